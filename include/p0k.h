@@ -1,0 +1,161 @@
+/* p0k.h — C ABI of the MI355X-native `gemm` path of p0pc0rn-kernels.
+ *
+ * One library (libp0k.so, HIP on gfx950) replaces the WebGPU runtime and the WGSL GEMM generator of the reference:
+ *
+ *   reference (JavaScript / WebGPU)                         this ABI
+ *   -------------------------------------------------------  ---------------------------------------------
+ *   createGpu(opts)            src/core/gpu.js:15-20         p0k_ctx_create / p0k_ctx_destroy
+ *   Gpu.buffer(size)           src/core/gpu.js:87-110        p0k_alloc   (zeroed, 16-byte rounded, pooled)
+ *   Gpu.free(buf)              src/core/gpu.js:112-121       p0k_free
+ *   Gpu.upload(data,..,dst)    src/core/gpu.js:141-148       p0k_upload
+ *   Gpu.read(buf, off, size)   src/core/gpu.js:150-170       p0k_download (blocks until the stream is done)
+ *   Gpu.done()                 src/core/gpu.js:171-176       p0k_sync
+ *   Gpu.poolStats/drainPool    src/core/gpu.js:134-137       p0k_pool_stats / p0k_drain_pool
+ *   gemm(gpu, args)            src/ops/gemm.js:268-327       p0k_gemm (args: p0k_gemm_args, the fields of GemmArgs,
+ *                                                            types/index.d.ts:128-150, and of the uniform P, gemm.js:39-41)
+ *   argument errors of gemm    src/ops/gemm.js:31,271,283,313 p0k_gemm_check (host only, never touches the GPU)
+ *   rowstats(gpu, a)           src/ops/misc.js:16-44         p0k_rowstats (the (mean, rstd) feed of the rms / lnmod prologues)
+ *   defaultTune / DEFAULT_TILE src/core/tune.js:30-36, gemm.js:22  p0k_select_tile
+ *   (timing: performance.now around gpu.done(), bench/bench.js:69-78)  p0k_event_* (HIP events on the context's stream)
+ *
+ * Conventions
+ *   - Buffers are device pointers returned by p0k_alloc. Every operand is given as (buffer, offset, size); offsets of
+ *     x / w / y are in BYTES, offsets of the fp32 vectors (ev, stats, pv, bv, rope) are in FLOATS (stats: in ROWS of
+ *     two floats), exactly as in the reference's argument objects.
+ *   - Sizes are the bytes the caller owns from `buf` onwards (the whole buffer, like the reference's `buf._pf`). They are
+ *     required: p0k_gemm refuses any call whose reads or writes would leave them (the reference binds whole buffers and
+ *     relies on WebGPU's robust access; a HIP kernel has no such guard).
+ *   - Every call returns P0K_OK (0) or an error code; p0k_last_error() gives the message. Errors in the arguments are
+ *     found on the host before anything is launched, and nothing is launched then.
+ *   - All work of one context runs in order on one HIP stream (default priority). p0k_gemm only enqueues.
+ */
+#ifndef P0K_H
+#define P0K_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define P0K_ABI_VERSION 1
+
+/* ---- status codes */
+enum {
+  P0K_OK = 0,
+  P0K_E_ARG = 1,          /* bad argument (the reference throws Error(...) for these) */
+  P0K_E_HIP = 2,          /* a HIP runtime error (the reference's GpuError / device lost) */
+  P0K_E_NOMEM = 3,        /* device allocation failed */
+  P0K_E_UNSUPPORTED = 4,  /* a combination this build does not implement */
+};
+
+/* ---- weight encodings (docs/FORMAT.md of the reference; gemm.js:269-271 maps the strings) */
+enum { P0K_ENC_Q4G32A_T64 = 1, P0K_ENC_Q8G64S_T64 = 2, P0K_ENC_F16 = 3 };
+/* ---- prologues: how X is read (gemm.js:60-95); conv / conv3 come from args.conv.kind in the reference */
+enum { P0K_X_F16 = 0, P0K_X_LNMOD = 1, P0K_X_RMS = 2, P0K_X_CONV = 3, P0K_X_CONV3 = 4 };
+/* ---- epilogues: how Y is written (gemm.js:191-254) */
+enum { P0K_EPI_F16 = 0, P0K_EPI_F32 = 1, P0K_EPI_RESADD = 2, P0K_EPI_SWIGLU = 3, P0K_EPI_HEADS = 4, P0K_EPI_BIAS = 5,
+       P0K_EPI_ONORMGATE = 6 };
+enum { P0K_ACT_SILU = 0, P0K_ACT_GELU = 1 };                 /* args.act */
+enum { P0K_ROPE_INTERLEAVED = 0, P0K_ROPE_HALF = 1 };        /* args.heads.ropeMode: default / 'half' */
+enum { P0K_ACC_F32 = 0, P0K_ACC_F16 = 1 };                   /* args.acc (see p0k_gemm) */
+
+typedef struct p0k_ctx p0k_ctx;
+
+/* One GEMM call: Y[m, n] = epilogue( sum_k X'[m, k] * W[n, k] ), X' = prologue(X) rounded to fp16, W dequantised to fp16.
+ * Field names follow GemmArgs (types/index.d.ts:128-150) and the uniform P (gemm.js:39-41). Zero-initialise the struct
+ * (all-zero = the reference's defaults) and set struct_size = sizeof(p0k_gemm_args). */
+typedef struct p0k_gemm_args {
+  uint32_t struct_size;
+  /* w: {enc, buf, off, bytes, rows, cols, ld} */
+  int32_t w_enc;
+  const void *w_buf; uint64_t w_off, w_bytes;
+  uint32_t w_rows, w_cols, w_ld;             /* rows = Nw, cols = Ktot; ld: f16 row stride in halves (0 = cols) */
+  /* x: {buf, off, size, ld, k0, mode} */
+  const void *x_buf; uint64_t x_off, x_size;
+  uint32_t x_ld, x_k0;                       /* ld 0 = K */
+  int32_t x_mode;                            /* P0K_X_F16 | LNMOD | RMS; CONV / CONV3 for args.conv */
+  /* y: {buf, off, size, ld, n0} */
+  void *y_buf; uint64_t y_off, y_size;
+  uint32_t y_ld, y_n0;                       /* ld 0 = N */
+  uint32_t M, N, K;
+  int32_t epi, acc;
+  uint32_t tile_bm, tile_bn;                 /* args.tile; 0 = choose (p0k_select_tile) */
+  uint32_t wr0, wr1, wk0;
+  /* fp32 vectors: (buf, off in floats, size in bytes from buf) */
+  const float *ev_buf; uint32_t ev_off; uint64_t ev_size;          /* gate (resadd), bias (bias), norm weights (heads) */
+  const float *st_buf; uint32_t st_off; uint64_t st_size;          /* stats: (mean, rstd) rows; off in rows */
+  const float *pv_buf; uint32_t pv_off, pv_stride; uint64_t pv_size; /* prologue vectors: gamma / scale (+stride: shift) */
+  const float *bv_buf; uint32_t bv_off, bv_up; uint64_t bv_size;   /* bias of resadd / swiglu (up at +bv_up) */
+  const void *gt_buf; uint64_t gt_size;                            /* onormgate gate, fp16 [M][Ltot] */
+  const float *rope_buf; uint64_t rope_size;                       /* heads: RP[row][64][cos, sin] */
+  int32_t res, store, act;
+  /* heads: {Ltot, Hq, Hkv, rowOff, eps, ropeMode} (eps 0 = 1e-6, as gemm.js:319) */
+  uint32_t h_Ltot, h_Hq, h_Hkv, h_rowOff; float h_eps; int32_t h_rope_mode;
+  /* conv: {Hi, Wi, Ci, Ho, Wo, stride, padT, padL, ks, up2, gn, pn} (stride 0 = 1, ks 0 = 1) */
+  uint32_t c_Hi, c_Wi, c_Ci, c_Ho, c_Wo, c_stride, c_padT, c_padL, c_ks;
+  int32_t c_up2, c_gn, c_pn;
+} p0k_gemm_args;
+
+/* rowstats (src/ops/misc.js:37-44): ST[(st_off + r) * 2 + {0, 1}] = (mean, rstd) of rows r of an fp32 [rows][ld] matrix,
+ * columns [c0, c0 + cols); mode 0 = LayerNorm (mean, biased variance), 1 = RMSNorm (mean 0). */
+typedef struct p0k_rowstats_args {
+  uint32_t struct_size;
+  const void *x_buf; uint64_t x_off, x_size;  /* x_off in bytes */
+  uint32_t ld, c0, rows, cols;               /* ld 0 = cols */
+  int32_t mode; float eps;
+  float *st_buf; uint32_t st_off; uint64_t st_size;
+} p0k_rowstats_args;
+
+typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM, 1 = GEMV (M <= 16) */
+  p0k_tile;
+
+typedef struct p0k_pool_stats {
+  uint64_t alive, peak, pooled, high_water, max_buf;
+  uint64_t creates, reuses, evictions, live_buffers, pooled_buffers;
+} p0k_pool_stats;
+
+typedef struct p0k_device_info {
+  char name[64]; char arch[64];
+  int32_t cus, xcds_hint; uint64_t hbm_bytes; int32_t clock_khz, mem_clock_khz, mem_bus_width;
+} p0k_device_info;
+
+/* ---- library */
+int p0k_abi_version(void);
+const char *p0k_last_error(void);            /* message of the last failed call on this thread */
+
+/* ---- context (createGpu) */
+int p0k_ctx_create(int device, p0k_ctx **out);
+void p0k_ctx_destroy(p0k_ctx *ctx);
+int p0k_device_info_get(p0k_ctx *ctx, p0k_device_info *out);
+
+/* ---- buffers */
+int p0k_alloc(p0k_ctx *ctx, uint64_t bytes, void **out);        /* zeroed; reuses a pooled buffer of the same rounded size */
+int p0k_free(p0k_ctx *ctx, void *buf);                          /* back to the pool (or released) */
+int p0k_drain_pool(p0k_ctx *ctx);
+int p0k_pool_stats_get(p0k_ctx *ctx, p0k_pool_stats *out);
+int p0k_upload(p0k_ctx *ctx, void *dst, uint64_t dst_off, const void *src, uint64_t n);
+int p0k_download(p0k_ctx *ctx, const void *src, uint64_t src_off, void *dst, uint64_t n);
+int p0k_copy(p0k_ctx *ctx, void *dst, uint64_t dst_off, const void *src, uint64_t src_off, uint64_t n);
+int p0k_sync(p0k_ctx *ctx);
+
+/* ---- the op */
+int p0k_gemm_check(const p0k_gemm_args *a);                    /* validation only (no context, no GPU) */
+int p0k_gemm(p0k_ctx *ctx, const p0k_gemm_args *a);            /* validate + enqueue; returns the status */
+double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the reference's return value (gemm.js:326) */
+int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use */
+int p0k_rowstats_check(const p0k_rowstats_args *a);
+int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
+
+/* ---- timing on the context's stream */
+typedef struct p0k_event p0k_event;
+int p0k_event_create(p0k_ctx *ctx, p0k_event **out);
+int p0k_event_record(p0k_ctx *ctx, p0k_event *ev);
+int p0k_event_elapsed_ms(p0k_event *start, p0k_event *stop, float *ms);   /* waits for stop */
+void p0k_event_destroy(p0k_event *ev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* P0K_H */

@@ -1,0 +1,251 @@
+// p0k_check.cpp — host-side argument validation of `gemm` and `rowstats`, and the translation of p0k_gemm_args into
+// the kernel Params. Pure host code: it never touches the GPU, so every error path is testable without one.
+//
+// The reference throws for: an unknown encoding (src/ops/gemm.js:271), K % 32 != 0 (:283), a bad tile (:31) and a
+// missing binding (:313). Those messages are kept. The reference binds whole WebGPU buffers and relies on robust buffer
+// access; a HIP kernel has none, so this build also refuses any call whose reads or writes leave the given buffer sizes,
+// and any alignment the 128-bit loads cannot honour (the reference's vec4 views need the same alignments, gemm.js:43-46).
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/p0k.h"
+#include "p0k_device.h"
+#include "p0k_internal.h"
+#include "p0k_launch.h"
+
+namespace p0k {
+
+static int fail(std::string *err, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(std::string *err, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (err) *err = buf;
+  return P0K_E_ARG;
+}
+
+static const char *epi_name(int e) {
+  static const char *n[] = {"f16", "f32", "resadd", "swiglu", "heads", "bias", "onormgate"};
+  return e >= 0 && e <= 6 ? n[e] : "?";
+}
+
+#define NEED(cond, ...) \
+  do {                  \
+    if (!(cond)) return fail(err, __VA_ARGS__); \
+  } while (0)
+#define FITS(what, need, have)                                                                                       \
+  do {                                                                                                               \
+    uint64_t n_ = (need), h_ = (have);                                                                               \
+    if (n_ > h_)                                                                                                     \
+      return fail(err, "gemm: %s needs %llu bytes from its offset, the buffer holds %llu", what, (unsigned long long)n_, \
+                  (unsigned long long)h_);                                                                            \
+  } while (0)
+
+// size of [off, end) available in a (buf, off, size) operand
+static uint64_t avail(uint64_t size, uint64_t off) { return size > off ? size - off : 0; }
+
+int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err) {
+  NEED(a != nullptr, "gemm: no arguments");
+  NEED(a->struct_size == sizeof(p0k_gemm_args), "gemm: struct_size %u, this library expects %u (ABI %d)", a->struct_size,
+       (unsigned)sizeof(p0k_gemm_args), P0K_ABI_VERSION);
+  const int we = a->w_enc;
+  NEED(we == P0K_ENC_Q4G32A_T64 || we == P0K_ENC_Q8G64S_T64 || we == P0K_ENC_F16, "gemm: unsupported weight encoding %d", we);
+  const uint32_t M = a->M, N = a->N, K = a->K;
+  NEED(K % 32 == 0, "gemm: K must be a multiple of 32");
+  const int epi = a->epi, xm = a->x_mode;
+  NEED(epi >= P0K_EPI_F16 && epi <= P0K_EPI_ONORMGATE, "gemm: unknown epilogue %d", epi);
+  NEED(xm >= P0K_X_F16 && xm <= P0K_X_CONV3, "gemm: unknown x mode %d", xm);
+  NEED(a->act == P0K_ACT_SILU || a->act == P0K_ACT_GELU, "gemm: unknown act %d", a->act);
+  NEED(a->h_rope_mode == P0K_ROPE_INTERLEAVED || a->h_rope_mode == P0K_ROPE_HALF, "gemm: unknown ropeMode %d", a->h_rope_mode);
+  NEED(a->acc == P0K_ACC_F32 || a->acc == P0K_ACC_F16, "gemm: unknown acc %d", a->acc);
+  if (a->tile_bm || a->tile_bn) {                                      // gemm.js:31 (heads / onormgate force BN = 128)
+    uint32_t bm = a->tile_bm, bn = (epi == P0K_EPI_HEADS || epi == P0K_EPI_ONORMGATE) ? 128 : a->tile_bn;
+    NEED(bm && bn && bm % 32 == 0 && bn % 64 == 0 && (bn / 8) * (bm / 8) <= 256, "bad tile %ux%u", a->tile_bm, a->tile_bn);
+  }
+  const bool xf32 = xm == P0K_X_LNMOD || xm == P0K_X_RMS, conv = xm == P0K_X_CONV, conv3 = xm == P0K_X_CONV3;
+  // ---- bindings the reference's kernel declares for this configuration (gemm.js:43-54, :313)
+  char key[96];
+  snprintf(key, sizeof key, "gemm.%d.%d.%s", we, xm, epi_name(epi));
+  NEED(a->x_buf, "gemm: missing binding X for %s", key);
+  NEED(a->w_buf, "gemm: missing binding W for %s", key);
+  NEED(a->y_buf, "gemm: missing binding Y for %s", key);
+  NEED(!(xf32 || (conv3 && a->c_pn)) || a->st_buf, "gemm: missing binding ST for %s", key);
+  NEED(!(xf32 || (conv && a->c_gn)) || a->pv_buf, "gemm: missing binding PV for %s", key);
+  NEED(!(epi == P0K_EPI_BIAS || epi == P0K_EPI_HEADS || epi == P0K_EPI_ONORMGATE) || a->ev_buf, "gemm: missing binding EV for %s", key);
+  NEED(epi != P0K_EPI_ONORMGATE || a->gt_buf, "gemm: missing binding GT for %s", key);
+  NEED(epi != P0K_EPI_HEADS || a->rope_buf, "gemm: missing binding RP for %s", key);
+
+  Params p;
+  memset(&p, 0, sizeof p);
+  p.M = M; p.N = N; p.K = K;
+  p.ldx = a->x_ld ? a->x_ld : K;
+  p.kx0 = a->x_k0;
+  p.wR0 = a->wr0; p.wR1 = a->wr1; p.wk0 = a->wk0;
+  p.ldy = a->y_ld ? a->y_ld : N;
+  p.ny0 = a->y_n0;
+  p.rowOff = a->h_rowOff; p.Ltot = a->h_Ltot; p.Hq = a->h_Hq; p.Hkv = a->h_Hkv;
+  p.eps = a->h_eps != 0.0f ? a->h_eps : 1e-6f;
+  p.pvOff = a->pv_buf ? a->pv_off : 0; p.pvStride = a->pv_buf ? a->pv_stride : 0;
+  p.evOff = a->ev_buf ? a->ev_off : 0; p.statOff = a->st_buf ? a->st_off : 0;
+  p.Hi = a->c_Hi; p.Wi = a->c_Wi; p.Ci = a->c_Ci; p.Ho = a->c_Ho; p.Wo = a->c_Wo;
+  p.stride = a->c_stride ? a->c_stride : 1; p.padT = a->c_padT; p.padL = a->c_padL; p.ks = a->c_ks ? a->c_ks : 1;
+  p.Nw = a->w_rows;
+  p.bvOff = a->bv_buf ? a->bv_off : 0; p.bvUp = a->bv_buf ? a->bv_up : 0;
+  p.epi = epi;
+  uint32_t f = 0;
+  if (a->ev_buf && epi == P0K_EPI_RESADD) f |= F_GATE;
+  if (a->bv_buf) f |= F_BIAS;
+  if (a->store) f |= F_STORE;
+  if (a->res) f |= F_RES;
+  if (a->act == P0K_ACT_GELU) f |= F_GELU;
+  if (a->h_rope_mode == P0K_ROPE_HALF) f |= F_ROPE_HALF;
+  if (conv3 && a->c_pn) f |= F_PN;
+  if (conv && a->c_gn) f |= F_GN;
+  if (conv && a->c_up2) f |= F_UP2;
+
+  // ---- weights
+  const uint32_t Nw = a->w_rows, Kt = a->w_cols;
+  NEED(Nw > 0 && Kt > 0, "gemm: w.rows and w.cols must be positive");
+  uint64_t wbytes;
+  if (we == P0K_ENC_Q4G32A_T64) {
+    NEED(Nw % 64 == 0 && Kt % 32 == 0, "gemm: q4g32a.t64 needs rows %% 64 == 0 and cols %% 32 == 0");
+    NEED(a->wk0 % 32 == 0, "gemm: wk0 must be a multiple of 32 for q4g32a.t64");
+    p.wG = Kt / 32;
+    wbytes = (uint64_t)(Nw / 64) * (Kt / 32) * 1280;
+    NEED(a->w_off % 16 == 0, "gemm: w.off must be 16-byte aligned");
+  } else if (we == P0K_ENC_Q8G64S_T64) {
+    NEED(Nw % 64 == 0 && Kt % 64 == 0, "gemm: q8g64s.t64 needs rows %% 64 == 0 and cols %% 64 == 0");
+    NEED(a->wk0 % 32 == 0, "gemm: wk0 must be a multiple of 32");
+    p.wG = Kt / 64;
+    wbytes = (uint64_t)(Nw / 64) * (Kt / 64) * 4224;
+    NEED(a->w_off % 16 == 0, "gemm: w.off must be 16-byte aligned");
+  } else {
+    p.wG = a->w_ld ? a->w_ld : Kt;
+    NEED(p.wG >= Kt, "gemm: w.ld (%u) < w.cols (%u)", p.wG, Kt);
+    NEED(p.wG % 4 == 0 && a->wk0 % 4 == 0 && a->w_off % 8 == 0, "gemm: f16 weights need w.ld, wk0 multiples of 4 and w.off of 8 bytes");
+    wbytes = ((uint64_t)(Nw - 1) * p.wG + Kt) * 2;
+    if (p.wG % 8 == 0 && a->wk0 % 8 == 0 && a->w_off % 16 == 0) f |= F_WALIGN8;
+  }
+  FITS("w", wbytes, a->w_bytes);
+  NEED((uint64_t)a->wk0 + K <= Kt, "gemm: wk0 + K (%llu) exceeds w.cols (%u)", (unsigned long long)a->wk0 + K, Kt);
+  if (epi == P0K_EPI_SWIGLU) {
+    NEED(N % 2 == 0, "gemm: swiglu needs an even N (gate and up columns interleave)");
+    NEED((uint64_t)a->wr0 + N / 2 <= Nw && (uint64_t)a->wr1 + N / 2 <= Nw, "gemm: swiglu rows wr0/wr1 + N/2 exceed w.rows");
+  }
+
+  // ---- X
+  const uint64_t xav = avail(a->x_size, 0);
+  if (xm == P0K_X_F16) {
+    NEED(p.ldx % 4 == 0 && p.kx0 % 4 == 0 && a->x_off % 8 == 0, "gemm: x.ld and x.k0 must be multiples of 4 (vec4 rows)");
+    if (M) FITS("x", a->x_off + ((uint64_t)(M - 1) * p.ldx + p.kx0 + K) * 2, xav);
+    if (p.ldx % 8 == 0 && p.kx0 % 8 == 0 && a->x_off % 16 == 0) f |= F_XALIGN8;
+  } else if (xf32) {
+    NEED(p.ldx % 4 == 0 && p.kx0 % 4 == 0 && a->x_off % 16 == 0, "gemm: fp32 x needs x.ld, x.k0 multiples of 4 and a 16-byte x.off");
+    if (M) FITS("x", a->x_off + ((uint64_t)(M - 1) * p.ldx + p.kx0 + K) * 4, xav);
+    NEED(p.pvOff % 4 == 0 && p.pvStride % 4 == 0, "gemm: pv.off and pv.stride must be multiples of 4 floats");
+    FITS("stats", ((uint64_t)p.statOff + M) * 8, a->st_size);
+    uint64_t pvn = (uint64_t)p.pvOff + (xm == P0K_X_LNMOD ? p.pvStride : 0) + p.kx0 + K;
+    FITS("pv", pvn * 4, a->pv_size);
+  } else {
+    NEED(p.Ci > 0 && p.Ci % 32 == 0, "gemm: conv needs Ci %% 32 == 0 (one tap per 32-k step)");
+    NEED(p.Hi && p.Wi && p.Ho && p.Wo, "gemm: conv needs Hi, Wi, Ho, Wo");
+    NEED(a->x_off % 16 == 0, "gemm: conv x.off must be 16-byte aligned");
+    if (conv) {
+      NEED(K <= p.ks * p.ks * p.Ci, "gemm: conv K (%u) exceeds ks*ks*Ci", K);
+      FITS("x", a->x_off + (uint64_t)p.Hi * p.Wi * p.Ci * 2, xav);
+      if (a->c_gn) FITS("pv", ((uint64_t)p.pvOff + p.pvStride + p.Ci) * 4, a->pv_size);
+      NEED(!a->c_gn || (p.pvOff % 4 == 0 && p.pvStride % 4 == 0), "gemm: pv.off and pv.stride must be multiples of 4 floats");
+    } else {
+      NEED(K <= 27 * p.Ci, "gemm: conv3 K (%u) exceeds 27*Ci", K);
+      const uint32_t T = p.stride;
+      uint64_t frames;
+      if (M) {
+        uint64_t otmax = (uint64_t)(M - 1) / ((uint64_t)p.Ho * p.Wo);
+        int64_t lo = (int64_t)p.padT - 1, hi = (int64_t)otmax + p.padT + 1;
+        lo = lo < 0 ? 0 : (lo > T - 1 ? T - 1 : lo);
+        hi = hi < 0 ? 0 : (hi > T - 1 ? T - 1 : hi);
+        if (p.ks > 1) {
+          frames = p.ks;
+        } else {
+          NEED(lo >= (int64_t)p.padL, "gemm: conv3 reads clip frame %lld but the input buffer starts at frame padL=%u", (long long)lo, p.padL);
+          frames = (uint64_t)(hi - p.padL + 1);
+        }
+        FITS("x", a->x_off + frames * p.Hi * p.Wi * p.Ci * 2, xav);
+        if (a->c_pn) FITS("stats", frames * p.Hi * p.Wi * 4, a->st_size);
+      }
+    }
+  }
+
+  // ---- Y and the epilogue vectors
+  const uint64_t yav = avail(a->y_size, 0);
+  NEED(a->y_off % 4 == 0, "gemm: y.off must be a multiple of 4 bytes");
+  if (M && N) {
+    const uint64_t rowspan = (uint64_t)(M - 1) * p.ldy + p.ny0;
+    switch (epi) {
+    case P0K_EPI_F16: case P0K_EPI_BIAS:
+      FITS("y", a->y_off + (rowspan + N) * 2, yav); break;
+    case P0K_EPI_F32: case P0K_EPI_RESADD:
+      FITS("y", a->y_off + (rowspan + N) * 4, yav); break;
+    case P0K_EPI_SWIGLU:
+      FITS("y", a->y_off + (rowspan + N / 2) * 2, yav); break;
+    case P0K_EPI_ONORMGATE: {
+      NEED(N % 128 == 0, "gemm: onormgate needs N %% 128 == 0 (one head per 128 columns)");
+      FITS("y", a->y_off + (rowspan + N) * 2, yav);
+      FITS("gt", ((uint64_t)(M - 1) * p.Ltot + p.ny0 + N) * 2, a->gt_size);
+      FITS("ev", ((uint64_t)p.evOff + 128) * 4, a->ev_size);
+      break;
+    }
+    case P0K_EPI_HEADS: {
+      NEED(N % 128 == 0, "gemm: heads needs N %% 128 == 0 (one head per 128 columns)");
+      uint64_t hd = N / 128 - 1;
+      FITS("y", a->y_off + ((hd * p.Ltot + p.rowOff + M - 1) * 128 + 128) * 2, yav);
+      FITS("rope", ((uint64_t)p.rowOff + M) * 128 * 4, a->rope_size);
+      uint64_t nh = N / 128, evn = 0;
+      if (nh > p.Hq && p.Hkv > 0) evn = 256;
+      else if (p.Hq > 0) evn = 128;
+      if (evn) FITS("ev", ((uint64_t)p.evOff + evn) * 4, a->ev_size);
+      break;
+    }
+    }
+    if (epi == P0K_EPI_BIAS || (epi == P0K_EPI_RESADD && a->ev_buf)) FITS("ev", ((uint64_t)p.evOff + N) * 4, a->ev_size);
+    if (a->bv_buf && epi == P0K_EPI_RESADD) FITS("bv", ((uint64_t)p.bvOff + N) * 4, a->bv_size);
+    if (a->bv_buf && epi == P0K_EPI_SWIGLU) {
+      uint64_t e0 = (uint64_t)p.bvOff + N / 2, e1 = (uint64_t)p.bvOff + p.bvUp + N / 2;
+      FITS("bv", (e0 > e1 ? e0 : e1) * 4, a->bv_size);
+    }
+  }
+  p.flags = f;
+
+  // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M)
+  int kernel = K_MFMA;
+  if (M <= (uint32_t)GEMV_MAX_M && (xm == P0K_X_F16 || xf32)) {
+    if (we != P0K_ENC_Q8G64S_T64 || (K % 64 == 0 && a->wk0 % 64 == 0)) kernel = K_GEMV;
+  }
+  if (out) *out = p;
+  if (plan) { plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = kernel == K_MFMA ? 128 : 16; plan->bn = 128; }
+  return P0K_OK;
+}
+
+int prepare_rowstats(const p0k_rowstats_args *a, std::string *err) {
+  NEED(a != nullptr, "rowstats: no arguments");
+  NEED(a->struct_size == sizeof(p0k_rowstats_args), "rowstats: struct_size %u, this library expects %u", a->struct_size,
+       (unsigned)sizeof(p0k_rowstats_args));
+  NEED(a->x_buf && a->st_buf, "rowstats: missing x or st buffer");
+  NEED(a->mode == 0 || a->mode == 1, "rowstats: mode must be 0 (ln) or 1 (rms)");
+  NEED(a->cols > 0, "rowstats: cols must be positive");
+  NEED(a->x_off % 4 == 0, "rowstats: x.off must be a multiple of 4 bytes");
+  uint32_t ld = a->ld ? a->ld : a->cols;
+  if (a->rows) {
+    uint64_t need = a->x_off + ((uint64_t)(a->rows - 1) * ld + a->c0 + a->cols) * 4;
+    if (need > a->x_size) return fail(err, "rowstats: x needs %llu bytes, the buffer holds %llu", (unsigned long long)need, (unsigned long long)a->x_size);
+    uint64_t sneed = ((uint64_t)a->st_off + a->rows) * 8;
+    if (sneed > a->st_size) return fail(err, "rowstats: st needs %llu bytes, the buffer holds %llu", (unsigned long long)sneed, (unsigned long long)a->st_size);
+  }
+  return P0K_OK;
+}
+
+}  // namespace p0k

@@ -1,0 +1,14 @@
+// p0k_internal.h — host-side declarations shared by the runtime and the argument checker.
+#pragma once
+#include <string>
+
+#include "../../include/p0k.h"
+
+namespace p0k {
+struct Params;
+enum { K_MFMA = 0, K_GEMV = 1 };
+struct Plan { int kernel, we, xm; unsigned bm, bn; };
+// validate a gemm call and translate it to kernel parameters (device pointers are filled in by the caller)
+int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err);
+int prepare_rowstats(const p0k_rowstats_args *a, std::string *err);
+}  // namespace p0k

@@ -1,0 +1,363 @@
+// p0k_runtime.cpp — the C ABI (include/p0k.h): context, buffer pool, copies, events, and the gemm / rowstats entry
+// points. It stands where the reference's WebGPU runtime stands (src/core/gpu.js): one HIP device and one stream per
+// context instead of a GPUDevice and its queue, hipMalloc'd buffers in a size-keyed pool instead of GPUBuffers.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/p0k.h"
+#include "p0k_device.h"
+#include "p0k_internal.h"
+#include "p0k_launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int set_err(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+int hip_err(hipError_t e, const char *what) {
+  return set_err(P0K_E_HIP, std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+#define HIPCHK(call, what)                   \
+  do {                                       \
+    hipError_t e_ = (call);                  \
+    if (e_ != hipSuccess) return hip_err(e_, what); \
+  } while (0)
+
+struct PooledBuf { void *ptr; uint64_t seq; };
+
+}  // namespace
+
+struct p0k_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  // pool accounting, as src/core/gpu.js:33-34, 87-138: every live byte is counted; a freed buffer is kept for the next
+  // request of exactly the same (16-byte rounded) size while pooled + live stays within the high-water mark + the
+  // largest buffer; reused buffers are cleared before they are handed out again.
+  std::unordered_map<void *, uint64_t> live;
+  std::map<uint64_t, std::vector<PooledBuf>> pool;
+  uint64_t alive = 0, peak = 0, pooled = 0, hw = 0, max_buf = 0, seq = 0;
+  uint64_t creates = 0, reuses = 0, evictions = 0, pooled_n = 0;
+  uint64_t cap() const { return hw + max_buf; }
+};
+
+struct p0k_event { hipEvent_t ev; int device; };
+
+extern "C" {
+
+int p0k_abi_version(void) { return P0K_ABI_VERSION; }
+const char *p0k_last_error(void) { return g_err.c_str(); }
+
+int p0k_ctx_create(int device, p0k_ctx **out) {
+  if (!out) return set_err(P0K_E_ARG, "ctx_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  HIPCHK(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  if (device < 0 || device >= n) return set_err(P0K_E_ARG, "ctx_create: no HIP device " + std::to_string(device));
+  HIPCHK(hipSetDevice(device), "hipSetDevice");
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return set_err(P0K_E_UNSUPPORTED, std::string("ctx_create: this library is built for gfx950, the device is ") + prop.gcnArchName);
+  p0k_ctx *c = new p0k_ctx();
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) { delete c; return hip_err(e, "hipStreamCreate"); }
+  *out = c;
+  return P0K_OK;
+}
+
+void p0k_ctx_destroy(p0k_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto &kv : c->live) (void)hipFree(kv.first);
+  for (auto &kv : c->pool)
+    for (auto &b : kv.second) (void)hipFree(b.ptr);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int p0k_device_info_get(p0k_ctx *c, p0k_device_info *out) {
+  if (!c || !out) return set_err(P0K_E_ARG, "device_info: NULL argument");
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties");
+  memset(out, 0, sizeof *out);
+  snprintf(out->name, sizeof out->name, "%s", prop.name);
+  snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+  out->cus = prop.multiProcessorCount;
+  out->xcds_hint = 8;
+  out->hbm_bytes = prop.totalGlobalMem;
+  out->clock_khz = prop.clockRate;
+  out->mem_clock_khz = prop.memoryClockRate;
+  out->mem_bus_width = prop.memoryBusWidth;
+  return P0K_OK;
+}
+
+// ------------------------------------------------------------------------------------------------ buffers
+static void evict(p0k_ctx *c, uint64_t room) {     // release pooled buffers, oldest first, until at most `room` pooled
+  while (c->pooled > room) {
+    uint64_t best_size = 0; size_t best_i = 0; uint64_t best_seq = UINT64_MAX;
+    for (auto &kv : c->pool)
+      for (size_t i = 0; i < kv.second.size(); i++)
+        if (kv.second[i].seq < best_seq) { best_seq = kv.second[i].seq; best_size = kv.first; best_i = i; }
+    if (best_seq == UINT64_MAX) break;
+    auto &v = c->pool[best_size];
+    (void)hipFree(v[best_i].ptr);
+    v.erase(v.begin() + best_i);
+    if (v.empty()) c->pool.erase(best_size);
+    c->pooled -= best_size; c->pooled_n--; c->evictions++;
+  }
+}
+
+int p0k_alloc(p0k_ctx *c, uint64_t bytes, void **out) {
+  if (!c || !out) return set_err(P0K_E_ARG, "alloc: NULL argument");
+  *out = nullptr;
+  std::lock_guard<std::mutex> lk(c->mu);
+  uint64_t size = std::max<uint64_t>(16, (bytes + 15) / 16 * 16);
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  auto it = c->pool.find(size);
+  if (it != c->pool.end() && !it->second.empty()) {
+    void *p = it->second.back().ptr;
+    it->second.pop_back();
+    if (it->second.empty()) c->pool.erase(it);
+    c->pooled -= size; c->pooled_n--; c->reuses++;
+    HIPCHK(hipMemsetAsync(p, 0, size, c->stream), "hipMemsetAsync");   // cleared like a new buffer (gpu.js:96-97)
+    c->live[p] = size; c->alive += size;
+    c->peak = std::max(c->peak, c->alive); c->hw = std::max(c->hw, c->alive);
+    *out = p;
+    return P0K_OK;
+  }
+  uint64_t cap = std::max(c->cap(), c->alive + size);
+  evict(c, cap - c->alive - size);
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, size);
+  if (e != hipSuccess) {
+    evict(c, 0);                                   // retry once with the pool drained
+    e = hipMalloc(&p, size);
+    if (e != hipSuccess) return set_err(P0K_E_NOMEM, "alloc: hipMalloc(" + std::to_string(size) + ") failed: " + hipGetErrorString(e));
+  }
+  HIPCHK(hipMemsetAsync(p, 0, size, c->stream), "hipMemsetAsync");
+  c->live[p] = size; c->alive += size; c->creates++;
+  c->max_buf = std::max(c->max_buf, size);
+  c->peak = std::max(c->peak, c->alive); c->hw = std::max(c->hw, c->alive);
+  *out = p;
+  return P0K_OK;
+}
+
+int p0k_free(p0k_ctx *c, void *p) {
+  if (!c) return set_err(P0K_E_ARG, "free: NULL context");
+  if (!p) return P0K_OK;
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->live.find(p);
+  if (it == c->live.end()) return set_err(P0K_E_ARG, "free: not a live buffer of this context");
+  uint64_t size = it->second;
+  c->live.erase(it);
+  c->alive -= size;
+  // a pooled buffer is only handed out again through p0k_alloc, whose clear is queued on the same stream after any
+  // work still reading it, so no wait is needed here
+  if (c->alive + c->pooled + size <= c->cap()) {
+    c->pool[size].push_back({p, ++c->seq});
+    c->pooled += size; c->pooled_n++;
+    return P0K_OK;
+  }
+  HIPCHK(hipFree(p), "hipFree");
+  return P0K_OK;
+}
+
+int p0k_drain_pool(p0k_ctx *c) {
+  if (!c) return set_err(P0K_E_ARG, "drain_pool: NULL context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  evict(c, 0);
+  return P0K_OK;
+}
+
+int p0k_pool_stats_get(p0k_ctx *c, p0k_pool_stats *s) {
+  if (!c || !s) return set_err(P0K_E_ARG, "pool_stats: NULL argument");
+  std::lock_guard<std::mutex> lk(c->mu);
+  s->alive = c->alive; s->peak = c->peak; s->pooled = c->pooled; s->high_water = c->hw; s->max_buf = c->max_buf;
+  s->creates = c->creates; s->reuses = c->reuses; s->evictions = c->evictions;
+  s->live_buffers = c->live.size(); s->pooled_buffers = c->pooled_n;
+  return P0K_OK;
+}
+
+static int check_range(p0k_ctx *c, const void *buf, uint64_t off, uint64_t n, const char *what) {
+  auto it = c->live.find(const_cast<void *>(buf));
+  if (it == c->live.end()) return set_err(P0K_E_ARG, std::string(what) + ": not a live buffer of this context");
+  if (off > it->second || n > it->second - off)
+    return set_err(P0K_E_ARG, std::string(what) + ": range [" + std::to_string(off) + ", +" + std::to_string(n) +
+                                  ") outside the buffer of " + std::to_string(it->second) + " bytes");
+  return P0K_OK;
+}
+
+int p0k_upload(p0k_ctx *c, void *dst, uint64_t off, const void *src, uint64_t n) {
+  if (!c || !dst || (!src && n)) return set_err(P0K_E_ARG, "upload: NULL argument");
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (int r = check_range(c, dst, off, n, "upload")) return r;
+  }
+  if (!n) return P0K_OK;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  HIPCHK(hipMemcpyAsync((uint8_t *)dst + off, src, n, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync H2D");
+  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");   // the host memory may be reused on return
+  return P0K_OK;
+}
+
+int p0k_download(p0k_ctx *c, const void *src, uint64_t off, void *dst, uint64_t n) {
+  if (!c || !src || (!dst && n)) return set_err(P0K_E_ARG, "download: NULL argument");
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (int r = check_range(c, src, off, n, "download")) return r;
+  }
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  if (n) HIPCHK(hipMemcpyAsync(dst, (const uint8_t *)src + off, n, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync D2H");
+  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return P0K_OK;
+}
+
+int p0k_copy(p0k_ctx *c, void *dst, uint64_t doff, const void *src, uint64_t soff, uint64_t n) {
+  if (!c || !dst || !src) return set_err(P0K_E_ARG, "copy: NULL argument");
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (int r = check_range(c, dst, doff, n, "copy dst")) return r;
+    if (int r = check_range(c, src, soff, n, "copy src")) return r;
+  }
+  if (!n) return P0K_OK;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  HIPCHK(hipMemcpyAsync((uint8_t *)dst + doff, (const uint8_t *)src + soff, n, hipMemcpyDeviceToDevice, c->stream),
+         "hipMemcpyAsync D2D");
+  return P0K_OK;
+}
+
+int p0k_sync(p0k_ctx *c) {
+  if (!c) return set_err(P0K_E_ARG, "sync: NULL context");
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return P0K_OK;
+}
+
+// ------------------------------------------------------------------------------------------------ the op
+int p0k_gemm_check(const p0k_gemm_args *a) {
+  std::string err;
+  int r = p0k::prepare_gemm(a, nullptr, nullptr, &err);
+  if (r) return set_err(r, err);
+  return P0K_OK;
+}
+
+double p0k_gemm_flops(const p0k_gemm_args *a) { return a ? 2.0 * a->M * a->N * a->K : 0.0; }
+
+int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out) {
+  std::string err;
+  p0k::Plan plan;
+  int r = p0k::prepare_gemm(a, nullptr, &plan, &err);
+  if (r) return set_err(r, err);
+  if (out) { out->bm = plan.bm; out->bn = plan.bn; out->kernel = plan.kernel; }
+  return P0K_OK;
+}
+
+// every operand must be a live buffer of this context, and its stated size must lie inside the allocation
+static int check_operand(p0k_ctx *c, const void *buf, uint64_t size, const char *what) {
+  if (!buf) return P0K_OK;
+  auto it = c->live.find(const_cast<void *>(buf));
+  if (it == c->live.end()) return set_err(P0K_E_ARG, std::string("gemm: ") + what + " is not a live buffer of this context");
+  if (size > it->second)
+    return set_err(P0K_E_ARG, std::string("gemm: ") + what + " size " + std::to_string(size) + " exceeds its allocation of " +
+                                  std::to_string(it->second) + " bytes");
+  return P0K_OK;
+}
+
+int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
+  if (!c) return set_err(P0K_E_ARG, "gemm: NULL context");
+  std::string err;
+  p0k::Params p;
+  p0k::Plan plan;
+  int r = p0k::prepare_gemm(a, &p, &plan, &err);
+  if (r) return set_err(r, err);
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    const struct { const void *b; uint64_t s; const char *n; } ops[] = {
+        {a->w_buf, a->w_off + a->w_bytes, "w"}, {a->x_buf, a->x_size, "x"}, {a->y_buf, a->y_size, "y"},
+        {a->ev_buf, a->ev_size, "ev"}, {a->st_buf, a->st_size, "stats"}, {a->pv_buf, a->pv_size, "pv"},
+        {a->bv_buf, a->bv_size, "bv"}, {a->gt_buf, a->gt_size, "gt"}, {a->rope_buf, a->rope_size, "rope"}};
+    for (auto &o : ops)
+      if (int rr = check_operand(c, o.b, o.s, o.n)) return rr;
+  }
+  if (a->M == 0 || a->N == 0) return P0K_OK;
+  p.W = (const uint8_t *)a->w_buf + a->w_off;
+  p.X = (const uint8_t *)a->x_buf + a->x_off;
+  p.Y = (uint8_t *)a->y_buf + a->y_off;
+  p.ST = a->st_buf; p.PV = a->pv_buf; p.EV = a->ev_buf; p.BV = a->bv_buf; p.RP = a->rope_buf;
+  p.GT = (const uint16_t *)a->gt_buf;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = plan.kernel == p0k::K_GEMV ? p0k::launch_gemv(p, plan.we, plan.xm, c->stream)
+                                             : p0k::launch_gemm_mfma(p, plan.we, plan.xm, c->stream);
+  if (e != hipSuccess) return hip_err(e, "gemm launch");
+  return P0K_OK;
+}
+
+int p0k_rowstats_check(const p0k_rowstats_args *a) {
+  std::string err;
+  int r = p0k::prepare_rowstats(a, &err);
+  if (r) return set_err(r, err);
+  return P0K_OK;
+}
+
+int p0k_rowstats(p0k_ctx *c, const p0k_rowstats_args *a) {
+  if (!c) return set_err(P0K_E_ARG, "rowstats: NULL context");
+  std::string err;
+  int r = p0k::prepare_rowstats(a, &err);
+  if (r) return set_err(r, err);
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto x = c->live.find(const_cast<void *>(a->x_buf)), s = c->live.find(a->st_buf);
+    if (x == c->live.end() || s == c->live.end()) return set_err(P0K_E_ARG, "rowstats: x / st are not live buffers of this context");
+    if (a->x_size > x->second || a->st_size > s->second) return set_err(P0K_E_ARG, "rowstats: a size exceeds its allocation");
+  }
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_rowstats((const uint8_t *)a->x_buf + a->x_off, a->ld ? a->ld : a->cols, a->c0, a->rows,
+                                      a->cols, a->mode, a->eps, a->st_buf, a->st_off, c->stream);
+  if (e != hipSuccess) return hip_err(e, "rowstats launch");
+  return P0K_OK;
+}
+
+// ------------------------------------------------------------------------------------------------ events
+int p0k_event_create(p0k_ctx *c, p0k_event **out) {
+  if (!c || !out) return set_err(P0K_E_ARG, "event_create: NULL argument");
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  p0k_event *ev = new p0k_event();
+  ev->device = c->device;
+  hipError_t e = hipEventCreate(&ev->ev);
+  if (e != hipSuccess) { delete ev; return hip_err(e, "hipEventCreate"); }
+  *out = ev;
+  return P0K_OK;
+}
+int p0k_event_record(p0k_ctx *c, p0k_event *ev) {
+  if (!c || !ev) return set_err(P0K_E_ARG, "event_record: NULL argument");
+  HIPCHK(hipEventRecord(ev->ev, c->stream), "hipEventRecord");
+  return P0K_OK;
+}
+int p0k_event_elapsed_ms(p0k_event *a, p0k_event *b, float *ms) {
+  if (!a || !b || !ms) return set_err(P0K_E_ARG, "event_elapsed: NULL argument");
+  HIPCHK(hipEventSynchronize(b->ev), "hipEventSynchronize");
+  HIPCHK(hipEventElapsedTime(ms, a->ev, b->ev), "hipEventElapsedTime");
+  return P0K_OK;
+}
+void p0k_event_destroy(p0k_event *ev) {
+  if (!ev) return;
+  (void)hipEventDestroy(ev->ev);
+  delete ev;
+}
+
+}  // extern "C"

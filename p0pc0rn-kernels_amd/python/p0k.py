@@ -1,0 +1,327 @@
+"""ctypes binding of libp0k.so (include/p0k.h) for the Python test and benchmark drivers.
+
+The argument objects follow the reference's GemmArgs (types/index.d.ts:128-150): a dict with
+``w: {enc, buf, off, bytes, rows, cols, ld}``, ``x: {buf, off, size, ld, k0, mode}``, ``y: {buf, off, size, ld, n0}``,
+``M, N, K, epi, acc, tile, wr0, wr1, wk0, ev, stats, pv, bv, gt, res, store, act, heads, conv``. Strings are the
+reference's ('q4g32a.t64', 'swiglu', 'gelu', 'half', ...). ``gemm_args(a, resolve)`` flattens such a dict into the C
+struct; ``resolve(buf)`` returns ``(pointer, size_in_bytes)`` of whatever stands for a buffer (a device Buffer here, a
+numpy array for the CPU oracle).
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "libp0k.so")
+
+ENC = {"q4g32a.t64": 1, "q8g64s.t64": 2, "f16": 3}
+XMODE = {"f16": 0, "lnmod": 1, "rms": 2, "conv": 3, "conv3": 4}
+EPI = {"f16": 0, "f32": 1, "resadd": 2, "swiglu": 3, "heads": 4, "bias": 5, "onormgate": 6}
+ACT = {"silu": 0, "gelu": 1}
+ACC = {"f32": 0, "f16": 1}
+
+OK, E_ARG, E_HIP, E_NOMEM, E_UNSUPPORTED = 0, 1, 2, 3, 4
+
+
+class GemmArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("w_enc", C.c_int32),
+        ("w_buf", C.c_void_p), ("w_off", C.c_uint64), ("w_bytes", C.c_uint64),
+        ("w_rows", C.c_uint32), ("w_cols", C.c_uint32), ("w_ld", C.c_uint32),
+        ("x_buf", C.c_void_p), ("x_off", C.c_uint64), ("x_size", C.c_uint64),
+        ("x_ld", C.c_uint32), ("x_k0", C.c_uint32),
+        ("x_mode", C.c_int32),
+        ("y_buf", C.c_void_p), ("y_off", C.c_uint64), ("y_size", C.c_uint64),
+        ("y_ld", C.c_uint32), ("y_n0", C.c_uint32),
+        ("M", C.c_uint32), ("N", C.c_uint32), ("K", C.c_uint32),
+        ("epi", C.c_int32), ("acc", C.c_int32),
+        ("tile_bm", C.c_uint32), ("tile_bn", C.c_uint32),
+        ("wr0", C.c_uint32), ("wr1", C.c_uint32), ("wk0", C.c_uint32),
+        ("ev_buf", C.c_void_p), ("ev_off", C.c_uint32), ("ev_size", C.c_uint64),
+        ("st_buf", C.c_void_p), ("st_off", C.c_uint32), ("st_size", C.c_uint64),
+        ("pv_buf", C.c_void_p), ("pv_off", C.c_uint32), ("pv_stride", C.c_uint32), ("pv_size", C.c_uint64),
+        ("bv_buf", C.c_void_p), ("bv_off", C.c_uint32), ("bv_up", C.c_uint32), ("bv_size", C.c_uint64),
+        ("gt_buf", C.c_void_p), ("gt_size", C.c_uint64),
+        ("rope_buf", C.c_void_p), ("rope_size", C.c_uint64),
+        ("res", C.c_int32), ("store", C.c_int32), ("act", C.c_int32),
+        ("h_Ltot", C.c_uint32), ("h_Hq", C.c_uint32), ("h_Hkv", C.c_uint32), ("h_rowOff", C.c_uint32),
+        ("h_eps", C.c_float), ("h_rope_mode", C.c_int32),
+        ("c_Hi", C.c_uint32), ("c_Wi", C.c_uint32), ("c_Ci", C.c_uint32), ("c_Ho", C.c_uint32), ("c_Wo", C.c_uint32),
+        ("c_stride", C.c_uint32), ("c_padT", C.c_uint32), ("c_padL", C.c_uint32), ("c_ks", C.c_uint32),
+        ("c_up2", C.c_int32), ("c_gn", C.c_int32), ("c_pn", C.c_int32),
+    ]
+
+
+class RowstatsArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("x_buf", C.c_void_p), ("x_off", C.c_uint64), ("x_size", C.c_uint64),
+        ("ld", C.c_uint32), ("c0", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+        ("mode", C.c_int32), ("eps", C.c_float),
+        ("st_buf", C.c_void_p), ("st_off", C.c_uint32), ("st_size", C.c_uint64),
+    ]
+
+
+class Tile(C.Structure):
+    _fields_ = [("bm", C.c_uint32), ("bn", C.c_uint32), ("kernel", C.c_int32)]
+
+
+class PoolStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("alive", "peak", "pooled", "high_water", "max_buf", "creates", "reuses",
+                                          "evictions", "live_buffers", "pooled_buffers")]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 64), ("cus", C.c_int32), ("xcds_hint", C.c_int32),
+                ("hbm_bytes", C.c_uint64), ("clock_khz", C.c_int32), ("mem_clock_khz", C.c_int32),
+                ("mem_bus_width", C.c_int32)]
+
+
+EXPORTS = [
+    "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
+    "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
+    "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
+    "p0k_event_create", "p0k_event_record", "p0k_event_elapsed_ms", "p0k_event_destroy",
+]
+
+_lib = None
+
+
+def lib():
+    """Load libp0k.so (fails loudly when it has not been built: there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python p0pc0rn-kernels_amd/build.py`")
+        L = C.CDLL(LIB_PATH)
+        P, U64, I = C.c_void_p, C.c_uint64, C.c_int
+        sigs = {
+            "p0k_abi_version": ([], I), "p0k_last_error": ([], C.c_char_p),
+            "p0k_ctx_create": ([I, C.POINTER(P)], I), "p0k_ctx_destroy": ([P], None),
+            "p0k_device_info_get": ([P, C.POINTER(DeviceInfo)], I),
+            "p0k_alloc": ([P, U64, C.POINTER(P)], I), "p0k_free": ([P, P], I), "p0k_drain_pool": ([P], I),
+            "p0k_pool_stats_get": ([P, C.POINTER(PoolStats)], I),
+            "p0k_upload": ([P, P, U64, P, U64], I), "p0k_download": ([P, P, U64, P, U64], I),
+            "p0k_copy": ([P, P, U64, P, U64, U64], I), "p0k_sync": ([P], I),
+            "p0k_gemm_check": ([C.POINTER(GemmArgs)], I), "p0k_gemm": ([P, C.POINTER(GemmArgs)], I),
+            "p0k_gemm_flops": ([C.POINTER(GemmArgs)], C.c_double),
+            "p0k_select_tile": ([C.POINTER(GemmArgs), C.POINTER(Tile)], I),
+            "p0k_rowstats_check": ([C.POINTER(RowstatsArgs)], I), "p0k_rowstats": ([P, C.POINTER(RowstatsArgs)], I),
+            "p0k_event_create": ([P, C.POINTER(P)], I), "p0k_event_record": ([P, P], I),
+            "p0k_event_elapsed_ms": ([P, P, C.POINTER(C.c_float)], I), "p0k_event_destroy": ([P], None),
+        }
+        for name, (args, res) in sigs.items():
+            fn = getattr(L, name)
+            fn.argtypes, fn.restype = args, res
+        _lib = L
+    return _lib
+
+
+class P0kError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+def _chk(code):
+    if code != OK:
+        raise P0kError(code, lib().p0k_last_error().decode())
+
+
+# ---------------------------------------------------------------------------------------------- argument objects
+def _get(d, k, default=None):
+    if d is None:
+        return default
+    v = d.get(k, default)
+    return default if v is None else v
+
+
+def gemm_args(a, resolve):
+    """Flatten a reference-style GemmArgs dict into GemmArgs. resolve(buf) -> (pointer, size)."""
+    s = GemmArgs()
+    s.struct_size = C.sizeof(GemmArgs)
+    w = a["w"]
+    if w["enc"] not in ENC:
+        s.w_enc = 0
+    else:
+        s.w_enc = ENC[w["enc"]]
+    wp, wsz = resolve(w["buf"])
+    s.w_buf, s.w_off = wp, _get(w, "off", 0)
+    s.w_bytes = _get(w, "bytes", wsz - s.w_off)
+    s.w_rows, s.w_cols, s.w_ld = w["rows"], w["cols"], _get(w, "ld", 0)
+    x = a["x"]
+    s.x_buf, s.x_size = resolve(x["buf"])
+    if x.get("size") is not None:
+        s.x_size = x["size"] + _get(x, "off", 0)
+    s.x_off, s.x_ld, s.x_k0 = _get(x, "off", 0), _get(x, "ld", 0), _get(x, "k0", 0)
+    cv = a.get("conv")
+    if cv:
+        s.x_mode = XMODE["conv3" if cv.get("kind") == "conv3" else "conv"]
+        s.c_Hi, s.c_Wi, s.c_Ci, s.c_Ho, s.c_Wo = cv["Hi"], cv["Wi"], cv["Ci"], cv["Ho"], cv["Wo"]
+        s.c_stride, s.c_padT, s.c_padL, s.c_ks = _get(cv, "stride", 1), _get(cv, "padT", 0), _get(cv, "padL", 0), _get(cv, "ks", 1)
+        s.c_up2, s.c_gn, s.c_pn = int(bool(cv.get("up2"))), int(bool(cv.get("gn"))), int(bool(cv.get("pn")))
+    else:
+        s.x_mode = XMODE[_get(x, "mode", "f16")]
+    y = a["y"]
+    s.y_buf, s.y_size = resolve(y["buf"])
+    if y.get("size") is not None:
+        s.y_size = y["size"] + _get(y, "off", 0)
+    s.y_off, s.y_ld, s.y_n0 = _get(y, "off", 0), _get(y, "ld", 0), _get(y, "n0", 0)
+    s.M, s.N, s.K = a["M"], a["N"], a["K"]
+    s.epi = EPI.get(a.get("epi") or "f16", -1)
+    s.acc = ACC[a.get("acc") or "f32"]
+    t = a.get("tile")
+    if t:
+        s.tile_bm, s.tile_bn = t["BM"], t["BN"]
+    s.wr0, s.wr1, s.wk0 = _get(a, "wr0", 0), _get(a, "wr1", 0), _get(a, "wk0", 0)
+    for key, pfx in (("ev", "ev"), ("stats", "st"), ("pv", "pv"), ("bv", "bv")):
+        v = a.get(key)
+        if v:
+            p, sz = resolve(v["buf"])
+            setattr(s, pfx + "_buf", p)
+            setattr(s, pfx + "_size", sz)
+            setattr(s, pfx + "_off", _get(v, "off", 0))
+            if key == "pv":
+                s.pv_stride = _get(v, "stride", 0)
+            if key == "bv":
+                s.bv_up = _get(v, "up", 0)
+    if a.get("gt"):
+        s.gt_buf, s.gt_size = resolve(a["gt"]["buf"])
+    s.res, s.store = int(bool(a.get("res"))), int(bool(a.get("store")))
+    s.act = ACT[a.get("act") or "silu"]
+    h = a.get("heads")
+    if h:
+        s.h_Ltot, s.h_Hq, s.h_Hkv, s.h_rowOff = h["Ltot"], h["Hq"], h["Hkv"], _get(h, "rowOff", 0)
+        s.h_eps = _get(h, "eps", 0.0)
+        s.h_rope_mode = 1 if h.get("ropeMode") == "half" else 0
+        if h.get("rope"):
+            s.rope_buf, s.rope_size = resolve(h["rope"]["buf"])
+    return s
+
+
+def numpy_resolve(arr):
+    """resolve() for host numpy arrays (the CPU oracle's buffers)."""
+    return arr.ctypes.data, arr.nbytes
+
+
+# ---------------------------------------------------------------------------------------------- device runtime
+class Buffer:
+    """A device buffer from p0k_alloc (the reference's GPUBuffer with `_pf` = its size)."""
+    __slots__ = ("ptr", "size", "dev")
+
+    def __init__(self, ptr, size, dev):
+        self.ptr, self.size, self.dev = ptr, size, dev
+
+
+class Device:
+    """createGpu() over libp0k: one HIP device, one stream."""
+
+    def __init__(self, device=0):
+        L = lib()
+        ctx = C.c_void_p()
+        _chk(L.p0k_ctx_create(device, C.byref(ctx)))
+        self.ctx = ctx
+
+    def close(self):
+        if self.ctx:
+            lib().p0k_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def info(self):
+        d = DeviceInfo()
+        _chk(lib().p0k_device_info_get(self.ctx, C.byref(d)))
+        return {"name": d.name.decode(), "arch": d.arch.decode(), "cus": d.cus, "hbm_bytes": d.hbm_bytes,
+                "clock_khz": d.clock_khz, "mem_clock_khz": d.mem_clock_khz, "mem_bus_width": d.mem_bus_width}
+
+    def buffer(self, nbytes):
+        p = C.c_void_p()
+        _chk(lib().p0k_alloc(self.ctx, int(nbytes), C.byref(p)))
+        return Buffer(p.value, max(16, (int(nbytes) + 15) // 16 * 16), self)
+
+    def upload(self, arr, dst=None, dst_off=0):
+        arr = np.ascontiguousarray(arr)
+        b = dst if dst is not None else self.buffer(arr.nbytes)
+        _chk(lib().p0k_upload(self.ctx, b.ptr, dst_off, arr.ctypes.data, arr.nbytes))
+        return b
+
+    def read(self, buf, dtype=np.uint8, count=None, off=0):
+        dtype = np.dtype(dtype)
+        n = (buf.size - off) // dtype.itemsize if count is None else count
+        out = np.empty(n, dtype=dtype)
+        _chk(lib().p0k_download(self.ctx, buf.ptr, off, out.ctypes.data, out.nbytes))
+        return out
+
+    def copy(self, dst, dst_off, src, src_off, n):
+        _chk(lib().p0k_copy(self.ctx, dst.ptr, dst_off, src.ptr, src_off, n))
+
+    def free(self, buf):
+        if buf is not None and buf.ptr:
+            _chk(lib().p0k_free(self.ctx, buf.ptr))
+            buf.ptr = None
+
+    def done(self):
+        _chk(lib().p0k_sync(self.ctx))
+
+    def pool_stats(self):
+        s = PoolStats()
+        _chk(lib().p0k_pool_stats_get(self.ctx, C.byref(s)))
+        return {n: getattr(s, n) for n, _ in PoolStats._fields_}
+
+    def drain_pool(self):
+        _chk(lib().p0k_drain_pool(self.ctx))
+
+    @staticmethod
+    def resolve(buf):
+        return buf.ptr, buf.size
+
+    def gemm(self, a):
+        """gemm(gpu, args) of src/ops/gemm.js:268: validate, enqueue, return the FLOPs (2MNK)."""
+        s = gemm_args(a, self.resolve)
+        _chk(lib().p0k_gemm(self.ctx, C.byref(s)))
+        return 2 * a["M"] * a["N"] * a["K"]
+
+    def gemm_raw(self, s):
+        _chk(lib().p0k_gemm(self.ctx, C.byref(s)))
+
+    def rowstats(self, x, rows, cols, mode, eps, st, ld=0, c0=0, st_off=0, x_off=0):
+        r = RowstatsArgs()
+        r.struct_size = C.sizeof(RowstatsArgs)
+        r.x_buf, r.x_off, r.x_size = x.ptr, x_off, x.size
+        r.ld, r.c0, r.rows, r.cols = ld, c0, rows, cols
+        r.mode, r.eps = (1 if mode == "rms" else 0), eps
+        r.st_buf, r.st_off, r.st_size = st.ptr, st_off, st.size
+        _chk(lib().p0k_rowstats(self.ctx, C.byref(r)))
+
+    # -- events on the context's stream
+    def event(self):
+        e = C.c_void_p()
+        _chk(lib().p0k_event_create(self.ctx, C.byref(e)))
+        return e
+
+    def record(self, e):
+        _chk(lib().p0k_event_record(self.ctx, e))
+
+    @staticmethod
+    def elapsed_ms(a, b):
+        ms = C.c_float()
+        _chk(lib().p0k_event_elapsed_ms(a, b, C.byref(ms)))
+        return ms.value
+
+    @staticmethod
+    def event_destroy(e):
+        lib().p0k_event_destroy(e)
+
+
+def check(a):
+    """Host-only validation of a GemmArgs dict (p0k_gemm_check); raises P0kError like the reference throws."""
+    s = gemm_args(a, lambda b: (b.ptr, b.size) if isinstance(b, Buffer) else numpy_resolve(b))
+    _chk(lib().p0k_gemm_check(C.byref(s)))
+
+
+def select_tile(a):
+    s = gemm_args(a, lambda b: (b.ptr, b.size) if isinstance(b, Buffer) else numpy_resolve(b))
+    t = Tile()
+    _chk(lib().p0k_select_tile(C.byref(s), C.byref(t)))
+    return {"BM": t.bm, "BN": t.bn, "kernel": "gemv" if t.kernel == 1 else "mfma"}

@@ -1,0 +1,135 @@
+"""The C ABI without a GPU: the library loads, exports every entry point include/p0k.h declares, the struct layout
+matches, and every argument error the reference throws (src/ops/gemm.js:31,271,283,313) — plus this build's bounds
+and alignment checks — is reported on the host before anything could launch."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import p0k
+from cases import make_case, make_conv3_case
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    txt = open(os.path.join(ROOT, "include", "p0k.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(p0k_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = p0k.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(L, n), f"{n} is declared in include/p0k.h but not exported"
+    assert set(names) == set(p0k.EXPORTS)
+    assert L.p0k_abi_version() == 1
+
+
+def test_struct_layout_matches():
+    a = p0k.GemmArgs()
+    a.struct_size = 7
+    assert p0k.lib().p0k_gemm_check(C.byref(a)) == p0k.E_ARG
+    msg = p0k.lib().p0k_last_error().decode()
+    want = int(re.search(r"expects (\d+)", msg).group(1))
+    assert want == C.sizeof(p0k.GemmArgs)
+
+
+def host_args(case):
+    return case.args(lambda n: case.bufs[n])
+
+
+def expect_error(a, pattern):
+    with pytest.raises(p0k.P0kError, match=pattern) as e:
+        p0k.check(a)
+    assert e.value.code == p0k.E_ARG
+
+
+def test_valid_cases_pass_check():
+    for kw in [dict(), dict(enc="q4g32a.t64", epi="swiglu", N=256), dict(enc="q8g64s.t64", xmode="rms", epi="resadd"),
+               dict(epi="heads", N=384, Hq=1, Hkv=1), dict(xmode="lnmod", epi="bias", res=True)]:
+        p0k.check(host_args(make_case(**kw)))
+    p0k.check(host_args(make_conv3_case()))
+
+
+def test_reference_errors():
+    c = make_case()
+    a = host_args(c)
+    a["w"]["enc"] = "q3"
+    expect_error(a, "unsupported weight encoding")
+    a = host_args(c)
+    a["K"] = 100
+    expect_error(a, "K must be a multiple of 32")
+    a = host_args(c)
+    a["tile"] = {"BM": 48, "BN": 128}
+    expect_error(a, "bad tile 48x128")
+    a["tile"] = {"BM": 256, "BN": 128}
+    expect_error(a, "bad tile")
+    a = host_args(make_case(epi="heads", N=384, Hq=1, Hkv=1))
+    a["tile"] = {"BM": 64, "BN": 64}                       # heads forces BN = 128: no error
+    p0k.check(a)
+
+
+def test_missing_bindings():
+    a = host_args(make_case(xmode="rms"))
+    del a["stats"]
+    expect_error(a, "missing binding ST")
+    a = host_args(make_case(xmode="lnmod"))
+    del a["pv"]
+    expect_error(a, "missing binding PV")
+    a = host_args(make_case(epi="bias"))
+    del a["ev"]
+    expect_error(a, "missing binding EV")
+    a = host_args(make_case(epi="heads", N=384, Hq=1, Hkv=1))
+    del a["heads"]["rope"]
+    expect_error(a, "missing binding RP")
+    a = host_args(make_case(epi="onormgate", N=256))
+    del a["gt"]
+    expect_error(a, "missing binding GT")
+
+
+def test_bounds_and_shapes():
+    a = host_args(make_case(M=8))
+    a["M"] = 9                                              # one row more than x holds
+    expect_error(a, "x needs")
+    a = host_args(make_case(M=8))
+    a["y"]["size"] = 100
+    expect_error(a, "y needs")
+    a = host_args(make_case(enc="q4g32a.t64"))
+    a["w"]["bytes"] -= 16
+    expect_error(a, "w needs")
+    a = host_args(make_case(enc="q4g32a.t64"))
+    a["wk0"] = 32
+    expect_error(a, "exceeds w.cols")
+    a = host_args(make_case(epi="swiglu", N=256))
+    a["N"] = 255
+    expect_error(a, "swiglu")
+    a = host_args(make_case(epi="heads", N=384, Hq=1, Hkv=1))
+    a["N"] = 320
+    expect_error(a, "heads needs N")
+    a = host_args(make_case(xmode="f16"))
+    a["x"]["ld"] = 258
+    expect_error(a, "multiples of 4")
+
+
+def test_conv3_frame_window_checked():
+    c = make_conv3_case()
+    a = host_args(c)
+    a["conv"]["padT"], a["conv"]["padL"] = 2, 2           # frame 1 is read but the buffer starts at frame 2
+    a["M"] = 36
+    expect_error(a, "starts at frame padL")
+    a = host_args(c)
+    a["conv"]["Ci"] = 16
+    expect_error(a, "Ci % 32")
+
+
+def test_kernel_choice():
+    assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv"
+    assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma"
+    c = make_conv3_case(T=1, H=2, W=2)                     # M = 4, a convolution: always the MFMA kernel
+    assert p0k.select_tile(host_args(c))["kernel"] == "mfma"
+    assert p0k.lib().p0k_gemm_flops(C.byref(p0k.gemm_args(host_args(make_case(M=3, N=64, K=32)), p0k.numpy_resolve))) == 2 * 3 * 64 * 32

@@ -1,0 +1,245 @@
+"""GPU parity of the HIP `gemm` path against the CPU oracle, through the C ABI (libp0k.so).
+
+Mirrors the reference's own GPU cases (test/kernels.test.js:71-145) — three encodings x two accumulate modes, partial
+tiles, the 3x3x3 convolution whole / per tile / in 2-frame chunks / from a 3-frame ring — and extends them to every
+prologue and epilogue of gemm.js on both kernels (the decode GEMV for M <= 16 and the MFMA GEMM above). Pass bars:
+the reference's cosine > 0.9995 against its fp32-weight cpuGemm, the per-element tolerance of cases.assert_close
+against the oracle, bit-identity where the reference demands it (conv3 chunks / ring), and bit-exact dequantised
+weights.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import p0k
+from cases import Case, assert_close, cos_maxerr, make_case, make_conv2d_case, make_conv3_case, to_float
+
+pytestmark = pytest.mark.gpu
+
+
+def banner(msg):
+    print(f"[p0k-test] {msg}", flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ reference suite
+@pytest.mark.parametrize("enc", ["f16", "q4g32a.t64", "q8g64s.t64"])
+@pytest.mark.parametrize("acc", ["f32", "f16"])
+def test_reference_gemm_cases(dev, enc, acc):
+    """test/kernels.test.js:72-84: M 32, N 128, K 256, X = f16(randn seed 7), W = randn(seed 11, 0.05)."""
+    M, N, K = 32, 128, 256
+    banner(f"reference gemm {enc} acc={acc}")
+    X = oracle.h2f(oracle.f16_bits(oracle.randn(M * K, 7)))
+    W0 = oracle.randn(N * K, 11, 0.05)
+    if enc == "f16":
+        Wd = oracle.h2f(oracle.f16_bits(W0))
+        wb = oracle.f16_bits(W0).view(np.uint8).copy()
+    else:
+        wb, Wd = (oracle.pack_q4 if enc.startswith("q4") else oracle.pack_q8)(W0, N, K, want_deq=True)
+    bufs = {"w": wb, "x": oracle.f16_bits(X), "y": np.zeros(M * N, np.uint16)}
+    spec = {"w": {"enc": enc, "buf": "w", "off": 0, "bytes": wb.nbytes, "rows": N, "cols": K}, "x": {"buf": "x"},
+            "y": {"buf": "y"}, "M": M, "N": N, "K": K, "acc": acc}
+    c = Case(spec, bufs)
+    got = c.run_device(dev)
+    cos, _ = cos_maxerr(to_float(got), oracle.cpu_gemm(X, Wd, M, N, K))
+    assert cos > 0.9995
+    assert_close(got, c.run_oracle(), what=f"{enc}/{acc}")
+
+
+def test_reference_partial_tiles(dev):
+    """test/kernels.test.js:85-92: M 33, N 192 (partial tiles), fp16 weights."""
+    M, N, K = 33, 192, 256
+    X = oracle.h2f(oracle.f16_bits(oracle.randn(M * K, 17)))
+    Wd = oracle.h2f(oracle.f16_bits(oracle.randn(N * K, 19, 0.05)))
+    bufs = {"w": oracle.f16_bits(Wd).view(np.uint8).copy(), "x": oracle.f16_bits(X), "y": np.zeros(M * N, np.uint16)}
+    spec = {"w": {"enc": "f16", "buf": "w", "off": 0, "bytes": bufs["w"].nbytes, "rows": N, "cols": K},
+            "x": {"buf": "x"}, "y": {"buf": "y"}, "M": M, "N": N, "K": K}
+    c = Case(spec, bufs)
+    got = c.run_device(dev)
+    cos, _ = cos_maxerr(to_float(got), oracle.cpu_gemm(X, Wd, M, N, K))
+    assert cos > 0.9995
+    assert_close(got, c.run_oracle())
+
+
+# ------------------------------------------------------------------------------------------------ all prologues/epilogues
+EPIS = [
+    ("f16", "f16", {}),
+    ("f16", "f32", {"ld_pad": 8, "k0": 32, "n0": 8}),
+    ("rms", "resadd", {"bias": True, "gate": True}),
+    ("lnmod", "resadd", {"store": True}),
+    ("f16", "resadd", {}),
+    ("lnmod", "bias", {"res": True}),
+    ("rms", "bias", {}),
+    ("f16", "swiglu", {}),
+    ("f16", "swiglu", {"act": "gelu", "bias": True}),
+    ("lnmod", "heads", {"Hq": 1, "Hkv": 1, "rope_mode": "half", "row_off": 3, "Ltot": 80}),
+    ("f16", "heads", {"Hq": 2, "Hkv": 1, "row_off": 1, "Ltot": 80}),
+    ("f16", "onormgate", {}),
+]
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 70])
+@pytest.mark.parametrize("enc", ["f16", "q4g32a.t64", "q8g64s.t64"])
+@pytest.mark.parametrize("xmode,epi,kw", EPIS, ids=[f"{x}-{e}-{i}" for i, (x, e, _) in enumerate(EPIS)])
+def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw):
+    kw = dict(kw)
+    N = {"heads": (kw.get("Hq", 1) + 2 * kw.get("Hkv", 1)) * 128, "swiglu": 384, "onormgate": 256}.get(epi, 192)
+    K = 256
+    banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
+    c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if M <= 16 else "mfma")
+    got = c.run_device(dev)
+    want = c.run_oracle()
+    assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
+
+
+# ------------------------------------------------------------------------------------------------ dequantisation
+def _adversarial_q4(rows, K, seed):
+    """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
+    rng = np.random.default_rng(seed)
+    u = rng.integers(0, 2 ** 32, size=(rows // 64) * (K // 32) * 320, dtype=np.uint64).astype(np.uint32).reshape(-1, 320)
+    s = rng.integers(0x0001, 0x5800, size=u[:, 256:].shape).astype(np.uint32)        # scales up to ~128, incl. subnormal
+    m = rng.integers(0x0000, 0x5C00, size=u[:, 256:].shape).astype(np.uint32) | (rng.integers(0, 2, size=s.shape).astype(np.uint32) << 15)
+    u[:, 256:] = s | (m << 16)
+    return u.ravel().view(np.uint8).copy()
+
+
+def _adversarial_q8(rows, K, seed):
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, size=(rows // 64) * (K // 64) * 4224, dtype=np.uint16).astype(np.uint8).reshape(-1, 4224)
+    sc = rng.integers(0x0001, 0x5000, size=(b.shape[0], 64)).astype(np.uint16)
+    b[:, 4096:] = sc.view(np.uint8).reshape(b.shape[0], 128)
+    return b.ravel().copy()
+
+
+@pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
+@pytest.mark.parametrize("path", ["gemv", "mfma"])
+def test_dequant_bit_exact(dev, enc, path):
+    """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
+    which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
+    to exercise both decoder paths."""
+    rows, K = 128, 128
+    wb = _adversarial_q4(rows, K, 3) if enc.startswith("q4") else _adversarial_q8(rows, K, 4)
+    want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
+    dw = dev.upload(wb)
+    try:
+        M = 16 if path == "gemv" else K
+        got = np.zeros((K, rows), np.uint16)
+        for k0 in range(0, K, M):
+            X = np.zeros((M, K), np.float32)
+            X[np.arange(M), k0 + np.arange(M)] = 1.0
+            dx = dev.upload(oracle.f16_bits(X))
+            dy = dev.buffer(M * rows * 2)
+            dev.gemm({"w": {"enc": enc, "buf": dw, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
+                      "x": {"buf": dx}, "y": {"buf": dy}, "M": M, "N": rows, "K": K})
+            got[k0:k0 + M] = dev.read(dy, np.uint16, M * rows).reshape(M, rows)
+            dev.free(dx)
+            dev.free(dy)
+        assert np.array_equal(got.T, want), f"{np.count_nonzero(got.T != want)} decoded weights differ"
+    finally:
+        dev.free(dw)
+
+
+# ------------------------------------------------------------------------------------------------ conv3 / conv
+def test_conv3_whole_clip(dev):
+    c = make_conv3_case()
+    T, H, W, C, N = c.dims
+    got = c.run_device(dev)
+    cos, _ = cos_maxerr(to_float(got), oracle.cpu_conv3(c.X, c.Wt, T, H, W, C, N))
+    assert cos > 0.9995
+    assert_close(got, c.run_oracle(), what="conv3")
+
+
+@pytest.mark.parametrize("tile", [{"BM": 128, "BN": 128}, {"BM": 64, "BN": 64}, {"BM": 32, "BN": 128}, {"BM": 128, "BN": 64}])
+def test_conv3_tiles(dev, tile):
+    """test/kernels.test.js:113-122: any tile the tuning table can pick gives the same (bit-identical) result."""
+    c = make_conv3_case()
+    base = c.run_device(dev)
+    c.spec["tile"] = tile
+    assert np.array_equal(c.run_device(dev), base)
+
+
+def _conv3_call(dev, c, dw, xbuf, xoff, ybuf, yoff, t0, nf, padL=0, ks=1):
+    T, H, W, C, N = c.dims
+    dev.gemm({"w": {"enc": c.spec["w"]["enc"], "buf": dw, "off": 0, "bytes": c.bufs["w"].nbytes, "rows": N, "cols": 27 * C},
+              "x": {"buf": xbuf, "off": xoff}, "y": {"buf": ybuf, "off": yoff}, "M": nf * H * W, "N": N, "K": 27 * C,
+              "conv": {"kind": "conv3", "Hi": H, "Wi": W, "Ci": C, "Ho": H, "Wo": W, "stride": T, "padT": t0,
+                       "padL": padL, "ks": ks}})
+
+
+@pytest.mark.parametrize("dims", [(5, 6, 6, 32, 128), (7, 5, 9, 64, 64)])
+def test_conv3_chunks_and_ring_bit_identical(dev, dims):
+    """test/kernels.test.js:123-145: 2-frame chunks and a 3-frame ring give output bit-identical to the whole clip."""
+    T, H, W, C, N = dims
+    c = make_conv3_case(T, H, W, C, N)
+    whole = c.run_device(dev)
+    fx, fy = H * W * C * 2, H * W * N * 2
+    dw, dx = dev.upload(c.bufs["w"]), dev.upload(c.bufs["x"])
+    ya, ring = dev.buffer(T * fy), dev.buffer(3 * fx)
+    try:
+        for t0 in range(0, T, 2):
+            padL = max(0, t0 - 1)
+            _conv3_call(dev, c, dw, dx, padL * fx, ya, t0 * fy, t0, min(2, T - t0), padL)
+        chunks = dev.read(ya, np.uint16, T * H * W * N)
+        assert np.array_equal(chunks, whole), "2-frame chunks differ from the whole clip"
+        yb = dev.buffer(T * fy)
+        for t in range(T):
+            for g in sorted({max(0, t - 1), t, min(T - 1, t + 1)}):
+                dev.copy(ring, (g % 3) * fx, dx, g * fx, fx)
+            _conv3_call(dev, c, dw, ring, 0, yb, t * fy, t, 1, 0, 3)
+            dev.done()
+        assert np.array_equal(dev.read(yb, np.uint16, T * H * W * N), whole), "3-frame ring differs from the whole clip"
+        dev.free(yb)
+    finally:
+        for b in (dw, dx, ya, ring):
+            dev.free(b)
+
+
+def test_conv3_pixelnorm(dev):
+    c = make_conv3_case(pn=True)
+    assert_close(c.run_device(dev), c.run_oracle(), what="conv3 pn")
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(stride=2), dict(up2=True), dict(gn=True), dict(ks=1, pad=0),
+                                dict(enc="q4g32a.t64", Ci=64, N=128)], ids=str)
+def test_conv2d(dev, kw):
+    c = make_conv2d_case(**kw)
+    assert_close(c.run_device(dev), c.run_oracle(), what=f"conv2d {kw}")
+
+
+# ------------------------------------------------------------------------------------------------ rowstats, runtime
+def test_rowstats(dev):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((37, 300)) * 2 + 0.5).astype(np.float32)
+    for mode in ("ln", "rms"):
+        want = np.zeros(80, np.float32)
+        oracle.rowstats(x, 37, 296, mode, 1e-6, want, ld=300, c0=4, st_off=3)
+        dx, ds = dev.upload(x), dev.buffer(80 * 4)
+        dev.rowstats(dx, 37, 296, mode, 1e-6, ds, ld=300, c0=4, st_off=3)
+        got = dev.read(ds, np.float32, 80)
+        assert np.allclose(got, want, rtol=2e-6, atol=2e-6)
+        dev.free(dx)
+        dev.free(ds)
+
+
+def test_pool_reuse_is_zeroed(dev):
+    b = dev.upload(np.arange(1000, dtype=np.float32))
+    size = b.size
+    dev.free(b)
+    c = dev.buffer(size)
+    assert np.all(dev.read(c, np.float32, 1000) == 0)
+    s = dev.pool_stats()
+    assert s["reuses"] >= 1
+    dev.free(c)
+
+
+def test_gemm_refuses_foreign_and_oversized_buffers(dev):
+    c = make_case(enc="f16", M=4, N=64, K=64)
+    d = {k: dev.upload(v) for k, v in c.bufs.items()}
+    try:
+        a = c.args(lambda n: d[n])
+        a["y"]["size"] = d["y"].size * 4
+        with pytest.raises(p0k.P0kError, match="exceeds its allocation|needs"):
+            dev.gemm(a)
+    finally:
+        for b in d.values():
+            dev.free(b)
