@@ -94,6 +94,8 @@ __device__ __forceinline__ void dq_q4_word(uint32_t w, uint32_t sm, bool fast, f
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       float a = fmaf((float)((w >> (4 * i)) & 15u), s, mn), b = fmaf((float)((w >> (4 * i + 16)) & 15u), s, mn);
+      // keep the fp32 rounding: without the barrier the compiler fuses fma + cvt into v_fma_mix (one rounding)
+      asm volatile("" : "+v"(a), "+v"(b));
       out[i] = (f16x2){(f16)a, (f16)b};
     }
   }
@@ -153,6 +155,7 @@ __device__ __forceinline__ u32x4 xload8(const Params &p, uint32_t row, const Row
     u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
     return (u32x4){lo.x, lo.y, hi.x, hi.y};
   } else if constexpr (XM == X_RMS || XM == X_LNMOD) {
+#pragma clang fp contract(off)   // one fp32 rounding per operation, in the reference's order, before the fp16 rounding
     const f32x4 *src = (const f32x4 *)(p.X + ((size_t)row * p.ldx + p.kx0 + k) * 4);
     f32x4 x0 = src[0], x1 = src[1];
     const float *st = p.ST + (size_t)(p.statOff + row) * 2;
