@@ -1,0 +1,316 @@
+"""Benchmark of the MI355X `gemm` path on BASELINE.json's configurations, one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME[,NAME]] [--no-cpu]
+
+A step is one gemm call (one pass of the hot path over one batch of synthetic input, all inputs resident in HBM).
+The headline line is the q4 GEMV decode with the SwiGLU epilogue at M = 1 (weight rows 28672 =
+gate 14336 | up 14336, K 4096): `value` is its HBM throughput in GB/s of algorithmic bytes. The same JSON line carries
+every other config (decode M = 4 and 16, q8 prefill with RMSNorm + residual, the DiT QKV / GeGLU GEMMs, conv3) under
+"workloads", each with its own roofline fraction.
+
+Timing: the timed calls are captured once in a HIP graph on the library's stream and replayed; HIP events on that
+stream bracket the replays (p0k_sync before and after). For the HBM-bound decode the calls rotate through enough
+weight copies (> 256 MB) that no call finds its weights in the MALL. Inputs come from numpy's PCG64 generator with
+fixed seeds, encoded with libp0k's own FORMAT.md encoders (BASELINE.json value recipes).
+
+cpu_baseline: the build's JavaScript restatement of the reference's CPU path (cpuGemm, float64 sums over dequantised
+fp32 weights, with the same prologue / epilogue formulas; oracle/cpu_ref.mjs) timed in Node on this host, one core,
+on a bounded row sample of the same workload, scaled linearly in M (the cost is exactly linear in M).
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "p0pc0rn-kernels_amd", "python"))
+import p0k  # noqa: E402
+
+HBM_PEAK = 8.0e12          # B/s, MI355X published
+FP16_PEAK = 2.5e15         # FLOP/s dense fp16 MFMA, MI355X published
+MALL = 256 << 20
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16)
+
+
+# ------------------------------------------------------------------------------------------------ workloads
+class Workload:
+    """Device buffers + a list of argument dicts (one per rotation copy) for one config."""
+
+    def __init__(self, name, desc, bound, flops, algo_bytes, M, args, bufs, extra=None):
+        self.name, self.desc, self.bound, self.flops, self.algo_bytes = name, desc, bound, flops, algo_bytes
+        self.M, self.args, self.bufs, self.extra = M, args, bufs, extra or {}
+
+
+def decode_q4(dev, M, copies=None):
+    """q4 GEMV decode, out 14336 with SwiGLU (weight rows [gate 14336 | up 14336]), K 4096."""
+    N_out, K = 14336, 4096
+    rows = 2 * N_out
+    r = rng(1)
+    W = (r.standard_normal((rows, K), dtype=np.float32) * np.float32(0.02))
+    wb = p0k.pack("q4g32a.t64", W, rows, K)
+    del W
+    copies = copies or max(4, -(-(2 * MALL) // wb.nbytes))
+    bufs = [dev.upload(wb) for _ in range(copies)]
+    x = dev.upload(f16(r.standard_normal(M * K)))
+    y = dev.buffer(M * N_out * 2)
+    bufs += [x, y]
+    args = [{"w": {"enc": "q4g32a.t64", "buf": b, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
+             "x": {"buf": x}, "y": {"buf": y}, "M": M, "N": rows, "K": K, "epi": "swiglu", "wr0": 0, "wr1": N_out}
+            for b in bufs[:copies]]
+    nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
+    return Workload(f"decode_q4_swiglu_M{M}", f"q4 GEMV + SwiGLU, M={M}, out {N_out}, weight rows {rows}, K={K}",
+                    "hbm", 2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
+
+
+def prefill_q8(dev):
+    """q8 GEMM M 2048 N 4096 K 4096, RMSNorm prologue (fp32 x, gamma 1+N(0,0.1), eps 1e-6 through
+    rowstats) and the fp32 residual-add epilogue (R N(0,1))."""
+    M, N, K = 2048, 4096, 4096
+    r = rng(2)
+    W = r.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wb = p0k.pack("q8g64s.t64", W, N, K)
+    del W
+    xw = dev.upload(f16(r.standard_normal(M * K)).astype(np.float32))
+    st = dev.buffer(M * 8)
+    dev.rowstats(xw, M, K, "rms", 1e-6, st)
+    gam = dev.upload((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
+    R = dev.upload(f16(r.standard_normal(M * N)).astype(np.float32))
+    w = dev.upload(wb)
+    args = [{"w": {"enc": "q8g64s.t64", "buf": w, "off": 0, "bytes": wb.nbytes, "rows": N, "cols": K},
+             "x": {"buf": xw, "mode": "rms"}, "stats": {"buf": st}, "pv": {"buf": gam},
+             "y": {"buf": R}, "M": M, "N": N, "K": K, "epi": "resadd"}]
+    nbytes = wb.nbytes + M * K * 4 + 2 * M * N * 4 + M * 8 + K * 4
+    return Workload("prefill_q8_rms_resadd", "q8 GEMM M=2048 N=4096 K=4096, RMSNorm prologue, fp32 residual add",
+                    "mfma", 2.0 * M * N * K, nbytes, M, args, [xw, st, gam, R, w])
+
+
+def rope2d(L, grid_w, theta=10000.0):
+    tok = np.arange(L)
+    y, x = tok // grid_w, tok % grid_w
+    inv = theta ** (-np.arange(32) / 32.0)
+    ang = np.concatenate([y[:, None] * inv, x[:, None] * inv], axis=1)
+    rp = np.empty((L, 64, 2), np.float32)
+    rp[..., 0], rp[..., 1] = np.cos(ang), np.sin(ang)
+    return rp.ravel()
+
+
+def dit_qkv(dev):
+    """configs[3](a): q4, M 4096 tokens (64x64 patches), K 3072, N 9216 = 24 Q + 24 K + 24 V heads of 128;
+    LayerNorm + adaLN prologue (shift / scale N(0, 0.5)) and the QK-RMSNorm + 2-D RoPE (theta 1e4) head split."""
+    M, N, K = 4096, 9216, 3072
+    r = rng(3)
+    W = r.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wb = p0k.pack("q4g32a.t64", W, N, K)
+    del W
+    xw = dev.upload(f16(r.standard_normal(M * K)).astype(np.float32))
+    st = dev.buffer(M * 8)
+    dev.rowstats(xw, M, K, "ln", 1e-6, st)
+    pv = dev.upload((0.5 * r.standard_normal(2 * K)).astype(np.float32))
+    ev = dev.upload((1 + 0.1 * r.standard_normal(256)).astype(np.float32))
+    rp = dev.upload(rope2d(M, 64))
+    w = dev.upload(wb)
+    y = dev.buffer(N * M * 2)
+    args = [{"w": {"enc": "q4g32a.t64", "buf": w, "off": 0, "bytes": wb.nbytes, "rows": N, "cols": K},
+             "x": {"buf": xw, "mode": "lnmod"}, "stats": {"buf": st}, "pv": {"buf": pv, "stride": K},
+             "ev": {"buf": ev}, "y": {"buf": y}, "M": M, "N": N, "K": K, "epi": "heads",
+             "heads": {"Ltot": M, "Hq": 24, "Hkv": 24, "eps": 1e-6, "rope": {"buf": rp}}}]
+    nbytes = wb.nbytes + M * K * 4 + M * N * 2 + M * 128 * 4
+    return Workload("dit_qkv_q4_lnmod_heads", "q4 M=4096 N=9216 K=3072, LN+adaLN prologue, QK-norm + 2-D RoPE heads",
+                    "mfma", 2.0 * M * N * K, nbytes, M, args, [xw, st, pv, ev, rp, w, y])
+
+
+def dit_up(dev):
+    """configs[3](b): q4 up-projection with the GeGLU epilogue, M 4096, K 3072, weight rows 24576 (gate | up)."""
+    M, K, N_out = 4096, 3072, 12288
+    rows = 2 * N_out
+    r = rng(4)
+    W = r.standard_normal((rows, K), dtype=np.float32) * np.float32(0.02)
+    wb = p0k.pack("q4g32a.t64", W, rows, K)
+    del W
+    x = dev.upload(f16(r.standard_normal(M * K)))
+    w = dev.upload(wb)
+    y = dev.buffer(M * N_out * 2)
+    args = [{"w": {"enc": "q4g32a.t64", "buf": w, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
+             "x": {"buf": x}, "y": {"buf": y}, "M": M, "N": rows, "K": K, "epi": "swiglu", "act": "gelu",
+             "wr0": 0, "wr1": N_out}]
+    nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
+    return Workload("dit_up_q4_geglu", "q4 M=4096 K=3072, weight rows 24576 (gate|up), GeGLU epilogue, out 12288",
+                    "mfma", 2.0 * M * rows * K, nbytes, M, args, [x, w, y])
+
+
+def conv3(dev):
+    """3x3x3 conv, Ci = Co = 128, clip T 13 x 92 x 160 (THWC fp16 N(0,1)), fp16 weights N(0, 0.02)."""
+    T, H, W, C, N = 13, 92, 160, 128, 128
+    K, M = 27 * C, T * H * W
+    r = rng(5)
+    wt = dev.upload(f16(0.02 * r.standard_normal(N * K)))
+    x = dev.upload(f16(r.standard_normal(M * C)))
+    y = dev.buffer(M * N * 2)
+    args = [{"w": {"enc": "f16", "buf": wt, "off": 0, "bytes": N * K * 2, "rows": N, "cols": K},
+             "x": {"buf": x}, "y": {"buf": y}, "M": M, "N": N, "K": K,
+             "conv": {"kind": "conv3", "Hi": H, "Wi": W, "Ci": C, "Ho": H, "Wo": W, "stride": T}}]
+    nbytes = N * K * 2 + M * C * 2 + M * N * 2
+    return Workload("conv3_128_T13x92x160", "3x3x3 conv 128->128 over a 13x92x160 clip, whole-clip call", "mfma",
+                    2.0 * M * N * K, nbytes, M, args, [wt, x, y])
+
+
+BUILDERS = {
+    "decode1": lambda d: decode_q4(d, 1), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
+    "prefill": prefill_q8, "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3,
+}
+
+
+# ------------------------------------------------------------------------------------------------ timing
+def time_workload(dev, wl, steps, warmup):
+    structs = [p0k.gemm_args(a, dev.resolve) for a in wl.args]
+    L = p0k.lib()
+    import ctypes as C
+    for s in structs:
+        p0k._chk(L.p0k_gemm_check(C.byref(s)))
+    per_graph = max(len(structs), min(steps, 64 if wl.bound == "hbm" else 8))
+    per_graph -= per_graph % len(structs)
+    dev.graph_begin()
+    try:
+        for i in range(per_graph):
+            dev.gemm_raw(structs[i % len(structs)])
+    finally:
+        g = dev.graph_end()
+    reps = max(1, -(-steps // per_graph))
+    for _ in range(max(1, -(-warmup // per_graph))):
+        dev.graph_launch(g)
+    dev.done()
+    e0, e1 = dev.event(), dev.event()
+    t0 = time.perf_counter()
+    dev.record(e0)
+    for _ in range(reps):
+        dev.graph_launch(g)
+    dev.record(e1)
+    dev.done()
+    wall = time.perf_counter() - t0
+    ms = dev.elapsed_ms(e0, e1)
+    dev.event_destroy(e0)
+    dev.event_destroy(e1)
+    dev.graph_destroy(g)
+    n = reps * per_graph
+    return ms / n, wall / n * 1e3, n
+
+
+def roofline(wl, ms):
+    sec = ms * 1e-3
+    if wl.bound == "hbm":
+        ach = wl.algo_bytes / sec / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": None}
+    ach = wl.flops / sec / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP16_PEAK / 1e12, "unit": "TFLOP/s",
+            "frac": round(ach * 1e12 / FP16_PEAK, 4), "traffic": None}
+
+
+# ------------------------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(config, rows):
+    """Run the JavaScript CPU restatement in Node on a row sample; returns its JSON report or None."""
+    script = os.path.join(ROOT, "oracle", "cpu_ref.mjs")
+    if not os.path.exists(script):
+        return None
+    try:
+        out = subprocess.run(["node", script, "bench", config, str(rows)], capture_output=True, text=True, timeout=240)
+    except (OSError, subprocess.TimeoutExpired) as e:
+        log(f"cpu baseline {config}: {e}")
+        return None
+    if out.returncode != 0:
+        log(f"cpu baseline {config} failed: {out.stderr[-400:]}")
+        return None
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+CPU_SAMPLE = {   # workload -> (cpu_ref config, rows of M timed)
+    "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 1), "decode_q4_swiglu_M16": ("decode", 1),
+    "prefill_q8_rms_resadd": ("prefill", 1), "dit_qkv_q4_lnmod_heads": ("dit_qkv", 1), "dit_up_q4_geglu": ("dit_up", 1),
+    "conv3_128_T13x92x160": ("conv3", 64),
+}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU (the gemm path has no multi-GPU mode here); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
+    dev = p0k.Device(0)
+    info = dev.info()
+    log(f"device {info}")
+    results = {}
+    for n in names:
+        wl = BUILDERS[n](dev)
+        steps = a.steps if wl.bound == "hbm" else max(10, a.steps // 10)
+        ms, wall_ms, count = time_workload(dev, wl, steps, a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10))
+        rf = roofline(wl, ms)
+        res = {"name": wl.name, "desc": wl.desc, "M": wl.M, "ms_per_call": round(ms, 5), "calls": count,
+               "tflops": round(wl.flops / ms / 1e9, 3), "gbps": round(wl.algo_bytes / ms / 1e6, 1),
+               "algo_bytes": wl.algo_bytes, "flops": wl.flops, "roofline": rf, **wl.extra}
+        log(f"{wl.name}: {ms * 1e3:.2f} us/call  {res['gbps']} GB/s  {res['tflops']} TFLOP/s  frac {rf['frac']}")
+        results[n] = res
+        for b in wl.bufs:
+            dev.free(b)
+        dev.drain_pool()
+    cores = 1
+    if not a.no_cpu:
+        cache = {}
+        for n, res in results.items():
+            cfg, rows = CPU_SAMPLE[res["name"]]
+            if (cfg, rows) not in cache:
+                cache[(cfg, rows)] = cpu_baseline(cfg, rows)
+            cb = cache[(cfg, rows)]
+            if cb:
+                cpu_ms = cb["deq_ms"] + cb["ms_per_row"] * res["M"]      # decode the weights once, then M rows
+                res["cpu"] = {"ms_per_call": cpu_ms, "sample_rows": cb["rows"], "sample_ms": cb["ms"],
+                              "node": cb.get("node"), "cpu_model": cb.get("cpu")}
+                res["x_vs_cpu"] = round(cpu_ms / res["ms_per_call"], 1)
+                log(f"cpu {res['name']}: {cpu_ms:.1f} ms/call (sample {cb['rows']} rows in {cb['ms']:.0f} ms) "
+                    f"-> x{res['x_vs_cpu']}")
+    head = results.get("decode1") or next(iter(results.values()))
+    hw = {k: v for k, v in head.items() if k not in ("roofline", "cpu")}
+    cpu = head.get("cpu")
+    line = {
+        "metric": "q4 GEMV decode + SwiGLU, HBM GB/s of algorithmic bytes (M=1, out 14336, K=4096)",
+        "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": head["calls"], "warmup": a.warmup,
+        "ms_per_step": head["ms_per_call"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4 weights (u4 codes -> fp16), fp16 activations, fp32 accumulate", "data": "synthetic (seeded PCG64)",
+        "config": {"workload": head["name"], "M": head["M"], "N": 28672, "K": 4096, "enc": "q4g32a.t64", "epi": "swiglu",
+                   "weight_copies_rotated": head.get("weight_copies")},
+        "roofline": head["roofline"],
+        "cpu_baseline": ({"value": round(head["algo_bytes"] / (cpu["ms_per_call"] * 1e6), 3), "unit": "GB/s",
+                          "cores": cores, "kind": "port",
+                          "sample": f"{cpu['sample_rows']} row(s) of M in {cpu['sample_ms']:.0f} ms, Node {cpu['node']}, "
+                                    f"{cpu['cpu_model']}, scaled x M"} if cpu else None),
+        "device": info["name"],
+        "workloads": list(results.values()),
+        "wall_ms_per_step": round(hw.get("ms_per_call", 0), 5),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

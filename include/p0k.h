@@ -148,6 +148,22 @@ int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel an
 int p0k_rowstats_check(const p0k_rowstats_args *a);
 int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
 
+/* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
+ *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */
+uint64_t p0k_tensor_bytes(int enc, uint32_t rows, uint32_t cols);
+int p0k_pack_q4(const float *W, uint32_t rows, uint32_t K, uint8_t *out, float *deq);
+int p0k_pack_q8(const float *W, uint32_t rows, uint32_t K, uint8_t *out, float *deq);
+int p0k_pack_f16(const float *W, uint64_t n, uint16_t *out);
+
+/* ---- HIP graphs: capture the context's stream (e.g. a decode step's gemm calls), then replay it with one launch.
+ *      (The reference batches dispatches into command buffers, src/core/gpu.js:203-257; a graph is the HIP form.)
+ *      Between begin and end only enqueueing calls may be made (p0k_gemm, p0k_rowstats, p0k_copy). */
+typedef struct p0k_graph p0k_graph;
+int p0k_graph_begin(p0k_ctx *ctx);
+int p0k_graph_end(p0k_ctx *ctx, p0k_graph **out);
+int p0k_graph_launch(p0k_ctx *ctx, p0k_graph *g);
+void p0k_graph_destroy(p0k_graph *g);
+
 /* ---- timing on the context's stream */
 typedef struct p0k_event p0k_event;
 int p0k_event_create(p0k_ctx *ctx, p0k_event **out);

@@ -332,6 +332,38 @@ int p0k_rowstats(p0k_ctx *c, const p0k_rowstats_args *a) {
   return P0K_OK;
 }
 
+// ------------------------------------------------------------------------------------------------ graphs
+struct p0k_graph { hipGraph_t graph; hipGraphExec_t exec; };
+
+int p0k_graph_begin(p0k_ctx *c) {
+  if (!c) return set_err(P0K_E_ARG, "graph_begin: NULL context");
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  return P0K_OK;
+}
+int p0k_graph_end(p0k_ctx *c, p0k_graph **out) {
+  if (!c || !out) return set_err(P0K_E_ARG, "graph_end: NULL argument");
+  *out = nullptr;
+  hipGraph_t g = nullptr;
+  HIPCHK(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+  hipGraphExec_t ex = nullptr;
+  hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) { (void)hipGraphDestroy(g); return hip_err(e, "hipGraphInstantiate"); }
+  *out = new p0k_graph{g, ex};
+  return P0K_OK;
+}
+int p0k_graph_launch(p0k_ctx *c, p0k_graph *g) {
+  if (!c || !g) return set_err(P0K_E_ARG, "graph_launch: NULL argument");
+  HIPCHK(hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+  return P0K_OK;
+}
+void p0k_graph_destroy(p0k_graph *g) {
+  if (!g) return;
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
 // ------------------------------------------------------------------------------------------------ events
 int p0k_event_create(p0k_ctx *c, p0k_event **out) {
   if (!c || !out) return set_err(P0K_E_ARG, "event_create: NULL argument");

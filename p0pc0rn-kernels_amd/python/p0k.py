@@ -84,6 +84,8 @@ EXPORTS = [
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
     "p0k_event_create", "p0k_event_record", "p0k_event_elapsed_ms", "p0k_event_destroy",
+    "p0k_tensor_bytes", "p0k_pack_q4", "p0k_pack_q8", "p0k_pack_f16",
+    "p0k_graph_begin", "p0k_graph_end", "p0k_graph_launch", "p0k_graph_destroy",
 ]
 
 _lib = None
@@ -111,6 +113,11 @@ def lib():
             "p0k_rowstats_check": ([C.POINTER(RowstatsArgs)], I), "p0k_rowstats": ([P, C.POINTER(RowstatsArgs)], I),
             "p0k_event_create": ([P, C.POINTER(P)], I), "p0k_event_record": ([P, P], I),
             "p0k_event_elapsed_ms": ([P, P, C.POINTER(C.c_float)], I), "p0k_event_destroy": ([P], None),
+            "p0k_tensor_bytes": ([I, C.c_uint32, C.c_uint32], U64),
+            "p0k_pack_q4": ([P, C.c_uint32, C.c_uint32, P, P], I), "p0k_pack_q8": ([P, C.c_uint32, C.c_uint32, P, P], I),
+            "p0k_pack_f16": ([P, U64, P], I),
+            "p0k_graph_begin": ([P], I), "p0k_graph_end": ([P, C.POINTER(P)], I), "p0k_graph_launch": ([P, P], I),
+            "p0k_graph_destroy": ([P], None),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(L, name)
@@ -312,6 +319,39 @@ class Device:
     @staticmethod
     def event_destroy(e):
         lib().p0k_event_destroy(e)
+
+    # -- graphs
+    def graph_begin(self):
+        _chk(lib().p0k_graph_begin(self.ctx))
+
+    def graph_end(self):
+        g = C.c_void_p()
+        _chk(lib().p0k_graph_end(self.ctx, C.byref(g)))
+        return g
+
+    def graph_launch(self, g):
+        _chk(lib().p0k_graph_launch(self.ctx, g))
+
+    @staticmethod
+    def graph_destroy(g):
+        lib().p0k_graph_destroy(g)
+
+
+# ---------------------------------------------------------------------------------------------- encoders (host CPU)
+def pack(enc, W, rows, K, want_deq=False):
+    """FORMAT.md encoders of libp0k (src/convert/encode.js:56-95): fp32 [rows][K] -> uint8 bytes (+ fp32 deq)."""
+    W = np.ascontiguousarray(W, dtype=np.float32).reshape(-1)
+    if enc == "f16":
+        out = np.empty(W.size, np.uint16)
+        _chk(lib().p0k_pack_f16(W.ctypes.data, W.size, out.ctypes.data))
+        return out.view(np.uint8)
+    out = np.zeros(lib().p0k_tensor_bytes(ENC[enc], rows, K), np.uint8)
+    deq = np.zeros(rows * K, np.float32) if want_deq else None
+    fn = lib().p0k_pack_q4 if enc == "q4g32a.t64" else lib().p0k_pack_q8
+    code = fn(W.ctypes.data, rows, K, out.ctypes.data, deq.ctypes.data if want_deq else None)
+    if code:
+        raise P0kError(code, f"{enc} needs rows % 64 == 0 and K % {32 if enc.startswith('q4') else 64} == 0")
+    return (out, deq) if want_deq else out
 
 
 def check(a):

@@ -133,3 +133,19 @@ def test_kernel_choice():
     c = make_conv3_case(T=1, H=2, W=2)                     # M = 4, a convolution: always the MFMA kernel
     assert p0k.select_tile(host_args(c))["kernel"] == "mfma"
     assert p0k.lib().p0k_gemm_flops(C.byref(p0k.gemm_args(host_args(make_case(M=3, N=64, K=32)), p0k.numpy_resolve))) == 2 * 3 * 64 * 32
+
+
+@pytest.mark.parametrize("enc,rows,K", [("q4g32a.t64", 128, 256), ("q8g64s.t64", 192, 128), ("f16", 64, 96)])
+def test_product_encoders_match_the_oracle(enc, rows, K):
+    """libp0k's host encoders (the converter side of FORMAT.md) produce the oracle's bytes exactly."""
+    import oracle
+    W = oracle.randn(rows * K, 77, 0.05)
+    W[5] = 0.0                                      # an all-zero group: scale 0 -> 1
+    if enc == "f16":
+        assert np.array_equal(p0k.pack(enc, W, rows, K), oracle.f16_bits(W).view(np.uint8))
+        return
+    got, gdeq = p0k.pack(enc, W, rows, K, want_deq=True)
+    want, wdeq = (oracle.pack_q4 if enc.startswith("q4") else oracle.pack_q8)(W, rows, K, want_deq=True)
+    assert np.array_equal(got, want) and np.array_equal(gdeq, wdeq)
+    with pytest.raises(p0k.P0kError):
+        p0k.pack(enc, W[: 32 * K], 32, K)
