@@ -70,8 +70,8 @@ def decode_q4(dev, M, copies=None):
     y = dev.buffer(M * N_out * 2)
     bufs += [x, y]
     args = [{"w": {"enc": "q4g32a.t64", "buf": b, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
-             "x": {"buf": x}, "y": {"buf": y}, "M": M, "N": rows, "K": K, "epi": "swiglu", "wr0": 0, "wr1": N_out}
-            for b in bufs[:copies]]
+             "x": {"buf": x}, "y": {"buf": y, "ld": N_out}, "M": M, "N": rows, "K": K, "epi": "swiglu", "wr0": 0,
+             "wr1": N_out} for b in bufs[:copies]]
     nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
     return Workload(f"decode_q4_swiglu_M{M}", f"q4 GEMV + SwiGLU, M={M}, out {N_out}, weight rows {rows}, K={K}",
                     "hbm", 2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
@@ -146,7 +146,7 @@ def dit_up(dev):
     w = dev.upload(wb)
     y = dev.buffer(M * N_out * 2)
     args = [{"w": {"enc": "q4g32a.t64", "buf": w, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
-             "x": {"buf": x}, "y": {"buf": y}, "M": M, "N": rows, "K": K, "epi": "swiglu", "act": "gelu",
+             "x": {"buf": x}, "y": {"buf": y, "ld": N_out}, "M": M, "N": rows, "K": K, "epi": "swiglu", "act": "gelu",
              "wr0": 0, "wr1": N_out}]
     nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
     return Workload("dit_up_q4_geglu", "q4 M=4096 K=3072, weight rows 24576 (gate|up), GeGLU epilogue, out 12288",
@@ -182,6 +182,19 @@ def time_workload(dev, wl, steps, warmup):
     import ctypes as C
     for s in structs:
         p0k._chk(L.p0k_gemm_check(C.byref(s)))
+        dev.gemm_raw(s)                 # one eager call per shape first: sizes the workspace before capture
+    dev.done()
+    if os.environ.get("P0K_BENCH_EAGER"):            # profiling: plain launches, no graph
+        e0, e1 = dev.event(), dev.event()
+        dev.record(e0)
+        for i in range(steps):
+            dev.gemm_raw(structs[i % len(structs)])
+        dev.record(e1)
+        dev.done()
+        ms = dev.elapsed_ms(e0, e1) / steps
+        dev.event_destroy(e0)
+        dev.event_destroy(e1)
+        return ms, ms, steps
     per_graph = max(len(structs), min(steps, 64 if wl.bound == "hbm" else 8))
     per_graph -= per_graph % len(structs)
     dev.graph_begin()

@@ -39,7 +39,8 @@ const rf16 = (v) => H2F[f2h(v)];
 
 // ------------------------------------------------------------------ weights (docs/FORMAT.md)
 const ENC = { 1: 'q4', 2: 'q8', 3: 'f16' };
-/** the fp16 weight value W'(r, kc) for kc in [k0, k0 + K) into out[o ..] (gemm.js:143-172) */
+/** the dequantised weights W(r, kc), kc in [k0, k0 + K), into out[o ..]: the fp32 values the test suite's encoders
+ *  hand to cpuGemm (src/convert/encode.js:68,85: F(q*s + mn), F(q*s)); fp16 weights as stored */
 function weightRow(enc, w, dv, wG, r, k0, K, out, o) {
   if (enc === 'q4') {
     for (let k = 0; k < K; k += 32) {
@@ -47,15 +48,15 @@ function weightRow(enc, w, dv, wG, r, k0, K, out, o) {
       const sm = dv.getUint32(rec + 1024 + rr * 4, true), s = H2F[sm & 0xffff], mn = H2F[sm >>> 16];
       for (let j = 0; j < 16; j++) {
         const b = w[rec + rr * 16 + j];
-        out[o + k + 2 * j] = rf16(F(F((b & 15) * s) + mn));
-        out[o + k + 2 * j + 1] = rf16(F(F((b >>> 4) * s) + mn));
+        out[o + k + 2 * j] = F(F((b & 15) * s) + mn);
+        out[o + k + 2 * j + 1] = F(F((b >>> 4) * s) + mn);
       }
     }
   } else if (enc === 'q8') {
     for (let k = 0; k < K; k += 32) {
       const kc = k0 + k, rec = ((r >>> 6) * wG + (kc >>> 6)) * 4224, rr = r & 63, hf = (kc >>> 5) & 1;
       const s = H2F[dv.getUint16(rec + 4096 + rr * 2, true)];
-      for (let i = 0; i < 32; i++) out[o + k + i] = rf16(F(((w[rec + rr * 64 + hf * 32 + i] << 24) >> 24) * s));
+      for (let i = 0; i < 32; i++) out[o + k + i] = F(((w[rec + rr * 64 + hf * 32 + i] << 24) >> 24) * s);
     }
   } else {
     for (let k = 0; k < K; k++) out[o + k] = H2F[dv.getUint16((r * wG + k0 + k) * 2, true)];

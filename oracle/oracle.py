@@ -46,6 +46,7 @@ def lib():
             ("or_randn", [P, C.c_int64, C.c_uint32, C.c_double], None),
             ("or_rand_uniform", [P, C.c_int64, C.c_uint32, F, F], None),
             ("or_gemm", [C.POINTER(p0k.GemmArgs), C.c_uint32, C.c_uint32], I),
+            ("or_set_weight_model", [I], None),
             ("or_rowstats", [C.POINTER(p0k.RowstatsArgs)], I),
             ("or_cpu_gemm", [P, P, I, I, I, P], None),
             ("or_cpu_conv3", [P, P, I, I, I, I, I, P], None),
@@ -123,10 +124,18 @@ def rand_uniform(n, seed, lo, hi):
     return out
 
 
-def gemm(a, m0=0, m1=None):
-    """Run rows [m0, m1) of a reference-style GemmArgs dict whose buffers are numpy arrays; Y is written in place."""
+KERNEL_WEIGHTS, CPU_WEIGHTS = 0, 1
+
+
+def gemm(a, m0=0, m1=None, weights=KERNEL_WEIGHTS):
+    """Run rows [m0, m1) of a reference-style GemmArgs dict whose buffers are numpy arrays; Y is written in place.
+    weights: KERNEL_WEIGHTS (fp16-rounded, the reference kernel) or CPU_WEIGHTS (fp32, the test suite's cpuGemm)."""
     s = p0k.gemm_args(a, p0k.numpy_resolve)
-    r = lib().or_gemm(C.byref(s), m0, a["M"] if m1 is None else m1)
+    lib().or_set_weight_model(weights)
+    try:
+        r = lib().or_gemm(C.byref(s), m0, a["M"] if m1 is None else m1)
+    finally:
+        lib().or_set_weight_model(KERNEL_WEIGHTS)
     if r:
         raise ValueError("oracle: bad gemm arguments")
 

@@ -183,6 +183,27 @@ void or_rand_uniform(float *out, int64_t n, uint32_t seed, float lo, float hi) {
   for (int64_t i = 0; i < n; i++) out[i] = (float)(lo + (hi - lo) * rng_next(&g));
 }
 
+/* ------------------------------------------------------------------ weight models
+ * 0: the reference kernel's: each dequantised weight rounded to fp16 (gemm.js:152,163)
+ * 1: the reference test suite's cpuGemm: the encoders' fp32 dequantised weights (src/convert/encode.js:68,85) */
+static int g_weight_model = 0;
+void or_set_weight_model(int m) { g_weight_model = m; }
+
+static float weight_value(int enc, const uint8_t *w, uint32_t wG, uint32_t r, uint32_t kc) {
+  if (g_weight_model == 1 && enc == P0K_ENC_Q4G32A_T64) {
+    const uint8_t *rec = w + ((uint64_t)(r >> 6) * wG + kc / 32) * 1280;
+    uint32_t rr = r & 63, kk = kc % 32;
+    uint32_t code = (rec[rr * 16 + kk / 2] >> ((kk & 1) * 4)) & 15, sm = get32(rec + 1024 + rr * 4);
+    return (float)((double)code * or_h2f((uint16_t)(sm & 0xffff)) + or_h2f((uint16_t)(sm >> 16)));
+  }
+  if (g_weight_model == 1 && enc == P0K_ENC_Q8G64S_T64) {
+    const uint8_t *rec = w + ((uint64_t)(r >> 6) * wG + kc / 64) * 4224;
+    uint32_t rr = r & 63, kk = kc % 64;
+    return (float)((double)(int8_t)rec[rr * 64 + kk] * or_h2f(get16(rec + 4096 + rr * 2)));
+  }
+  return or_h2f(or_weight_f16(enc, w, wG, r, kc));
+}
+
 /* ------------------------------------------------------------------ the GEMM (src/ops/gemm.js) */
 typedef struct {
   const p0k_gemm_args *a;
@@ -279,7 +300,7 @@ int or_gemm(const p0k_gemm_args *a, uint32_t m0, uint32_t m1) {
   float *Wd = (float *)malloc(sizeof(float) * (uint64_t)N * K);
   for (uint32_t n = 0; n < N; n++) {
     uint32_t r = wrow(&c, n);
-    for (uint32_t k = 0; k < K; k++) Wd[(uint64_t)n * K + k] = or_h2f(or_weight_f16(a->w_enc, wb, c.wG, r, a->wk0 + k));
+    for (uint32_t k = 0; k < K; k++) Wd[(uint64_t)n * K + k] = weight_value(a->w_enc, wb, c.wG, r, a->wk0 + k);
   }
   (void)wcol;
   for (uint32_t m = m0; m < m1; m++) {

@@ -37,6 +37,9 @@ void or_dequant(int enc, const uint8_t *w, int rows, int cols, uint16_t *out);
 void or_randn(float *out, int64_t n, uint32_t seed, double scale);
 void or_rand_uniform(float *out, int64_t n, uint32_t seed, float lo, float hi);
 
+/* which dequantised weights or_gemm multiplies by: 0 = fp16-rounded (the reference kernel, gemm.js:152,163; default),
+ * 1 = fp32 (the reference test suite's cpuGemm over the encoders' deq output, test/kernels.test.js:25-29) */
+void or_set_weight_model(int model);
 /* rows [m0, m1) of one gemm call (src/ops/gemm.js semantics), all buffers on the host; returns 0 or -1 (bad args) */
 int or_gemm(const p0k_gemm_args *a, uint32_t m0, uint32_t m1);
 /* src/ops/misc.js:16-44 */

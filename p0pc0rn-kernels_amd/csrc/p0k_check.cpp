@@ -7,6 +7,7 @@
 // and any alignment the 128-bit loads cannot honour (the reference's vec4 views need the same alignments, gemm.js:43-46).
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -222,11 +223,26 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
 
   // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M)
   int kernel = K_MFMA;
-  if (M <= (uint32_t)GEMV_MAX_M && (xm == P0K_X_F16 || xf32)) {
-    if (we != P0K_ENC_Q8G64S_T64 || (K % 64 == 0 && a->wk0 % 64 == 0)) kernel = K_GEMV;
+  unsigned S = 0, KS = 0;
+  if (M <= (uint32_t)GEMV_MAX_M && (xm == P0K_X_F16 || xf32) && M > 0) {
+    // the GEMV reads q8 in whole 64-k records and f16 rows with 16-byte loads only
+    // and addresses the tensor with 32-bit offsets
+    if ((we != P0K_ENC_Q8G64S_T64 || a->wk0 % 64 == 0) && (we != P0K_ENC_F16 || (f & F_WALIGN8)) &&
+        wbytes < (1ull << 32)) {
+      gemv_split(p, we, MI355X_CUS, &S, &KS);
+      // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
+      if (const char *ov = getenv("P0K_GEMV_SLICES")) {
+        unsigned s2 = (unsigned)atoi(ov), quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
+        if (s2 && K % (s2 * quant) == 0) { S = s2; KS = K / s2; }
+      }
+      if (S) kernel = K_GEMV;
+    }
   }
   if (out) *out = p;
-  if (plan) { plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = kernel == K_MFMA ? 128 : 16; plan->bn = 128; }
+  if (plan) {
+    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = kernel == K_MFMA ? 128 : 16; plan->bn = 128;
+    plan->S = S; plan->KS = KS;
+  }
   return P0K_OK;
 }
 

@@ -22,6 +22,7 @@ namespace p0k {
 typedef _Float16 f16;
 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -71,13 +72,12 @@ __device__ __forceinline__ uint32_t wrow(const Params &p, uint32_t n) {
 // exact in fp32: q*s has at most 15 significant bits, mn 11, so the sum fits fp32's 24 bits when the exponents satisfy
 // -8 <= E(mn) - E(s) <= 12 (or mn = 0). Other (scale, min) words take the fp32 path, which is the reference's formula.
 __device__ __forceinline__ bool q4_fast_ok(uint32_t sm) {
-  uint32_t sb = sm & 0xffffu, mb = sm >> 16;
-  int es = (sb >> 10) & 31, em = (mb >> 10) & 31;
-  if (es == 31 || em == 31) return false;
-  if ((mb & 0x7fffu) == 0u) return true;
-  es = es ? es : 1; em = em ? em : 1;
-  int d = em - es;
-  return d >= -8 && d <= 12;
+  // branch-free (it sits inside unrolled streaming loops): exponent fields, 0 counted as 1 (subnormals)
+  const uint32_t mb = sm >> 16;
+  const int es = (int)((sm >> 10) & 31u), em = (int)((mb >> 10) & 31u);
+  const int d = (em | (em == 0)) - (es | (es == 0));
+  const bool finite = (es != 31) & (em != 31);
+  return finite & (((mb & 0x7fffu) == 0u) | ((d >= -8) & (d <= 12)));
 }
 __device__ __forceinline__ void dq_q4_word(uint32_t w, uint32_t sm, bool fast, f16x2 out[4]) {
   if (fast) {

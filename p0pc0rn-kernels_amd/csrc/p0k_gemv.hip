@@ -1,190 +1,323 @@
 // p0k_gemv.hip — the decode path of `gemm` (M <= 16): memory-bound, so it is shaped around HBM, not the matrix cores.
 //
-// A workgroup owns 128 ws columns (for SwiGLU: 64 gate rows + the 64 matching up rows, i.e. one q4/q8 tile record
-// row-block each) and walks the whole K. Its 8 waves are 2 column halves x 4 K-slices. Lane l of a wave owns ONE
-// weight row: per 32-k (q4, f16) or 64-k (q8) unit it issues one 128-bit load of that row's codes (a wave reads a
-// whole 1 KB / 4 KB record row-block, coalesced) plus the row's scale word, decodes them in registers to fp16 pairs,
-// and accumulates v_dot2_f32_f16 against X' broadcast from LDS. So every lane has its own sum and no cross-lane
-// reduction is needed inside the K loop; the 4 K-slices meet once in LDS at the end.
+// Work items are (N-tile of 128 ws columns) x (K-slice). 128 ws columns are two 64-row record blocks of FORMAT.md
+// (for SwiGLU: 64 gate rows + the 64 matching up rows). Large N runs one slice per tile (S = 1); the host raises S
+// only when there are too few tiles to occupy the GPU or X' of the slice would not fit in LDS.
 //
-// X' (the prologue applied, rounded to fp16, gemm.js:60-67) is staged per 512-k chunk in LDS by the whole workgroup,
-// in the pair order of the weight encoding. The weight loads of chunk c+1 are issued before chunk c is computed.
+// An item is 8 waves = 2 column halves x 4 K-quarters. Lane l of a wave owns ONE weight row: per 32-k (q4, f16) or
+// 64-k (q8) unit it reads that row's codes with one 128-bit load (a wave reads a whole 1 KB / 4 KB record row-block,
+// coalesced) plus the row's scale word. Each wave streams its K range through a ring of PF units held in registers:
+// as soon as unit j is reduced its slot is refilled with unit j + PF, so PF loads stay in flight for the whole stream.
+// Every lane owns its own sum, so the stream has no cross-lane work and no barrier; the K-quarters meet in LDS at the
+// end. X' (the prologue applied, rounded to fp16 as in the reference) is staged in LDS once per item.
+//
+// The reduction never materialises fp16 weights; the decode is the VALU cost of this kernel, so it is kept to five
+// bit operations per 8 codes. For a q4 unit with codes q, scale s, minimum mn and the unit's X':
+//     sum_k x_k (q_k s + mn) = s * sum_k x_k q_k + mn * X,          X = sum_k x_k
+//     sum_k x_k q_k = (Dlo - 1024 Xlo) + (Dhi - 1024 Xhi) / 16
+// where the nibbles in bits 0-3 of a byte give the fp16 1024 + q (code | 0x6400), those in bits 4-7 give 1024 + 16 q
+// in place (no shift), Dlo / Dhi are v_dot2_f32_f16 sums over those pairs, and Xlo / Xhi are X' sums over the same
+// positions, computed once per item. q8: sum_k x_k q_k s = s * (D - 1152 X) with (byte ^ 0x80) | 0x6400 = 1152 + q.
+// This is the reference's CPU path (cpuGemm over fp32 dequantised weights, test/kernels.test.js:29) in fp32; the
+// reference kernel rounds each weight to fp16 first, and the two differ by less than that rounding. For x a unit
+// vector it returns f16(f32(q*s + mn)) / f16(q*s) exactly, the reference's dequantised weight.
+//
+// With S > 1 the slices of a tile meet through a workspace: each item writes its fp32 partial tile to the memory side,
+// bumps the tile's counter, and the item that arrives last sums the S partials in slice order 0..S-1 (the result does
+// not depend on which item finishes last), runs the epilogue and resets the counter to 0.
 #include "p0k_device.h"
 #include "p0k_launch.h"
 
 namespace p0k {
 
-constexpr int GV_NT = 512, GV_SUB = 4, GV_KC = 512;
+constexpr int GV_KSUB = 4, GV_NT = 2 * GV_KSUB * 64;     // 512 threads
+constexpr int GV_LDS = 40 * 1024;                       // X' of the slice and its group sums, then the partials
 
 template <int WE>
 struct Unit;
 template <>
-struct Unit<W_Q4> { static constexpr int UK = 32; u32x4 code; uint32_t sm; };
+struct Unit<W_Q4> { static constexpr int UK = 32, PF = 8; u32x4 code; uint32_t sm; };
 template <>
-struct Unit<W_Q8> { static constexpr int UK = 64; u32x4 code[4]; uint32_t s; };
+struct Unit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x4 code[4]; uint32_t s; };
 template <>
-struct Unit<W_F16> { static constexpr int UK = 32; u32x4 v[4]; };
+struct Unit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
+
+// longest slice whose X' (2 B per k and row) and group sums (2 floats per 32 k and row) fit the LDS budget
+template <int MT>
+constexpr int ks_max() { return (GV_LDS * 8 / (MT * 18)) & ~1023; }
 
 template <int WE, int XM, int MT>
-__global__ __launch_bounds__(GV_NT) void k_gemv(Params p) {
-  constexpr int UK = Unit<WE>::UK;
-  constexpr int UPW = (GV_KC / UK) / GV_SUB;          // units per wave per chunk
-  __shared__ __attribute__((aligned(16))) f16 sX[MT * GV_KC];
-  __shared__ __attribute__((aligned(16))) float sR[GV_SUB * MT * 128];
+__global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
+  constexpr int UK = Unit<WE>::UK, PF = Unit<WE>::PF, KSM = ks_max<MT>(), NGM = KSM / UK;
+  static_assert(GV_KSUB * MT * 128 * 4 <= GV_LDS, "partials must fit the staging buffer");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GV_LDS];
+  __shared__ uint32_t sLast;
+  f16 *sX = (f16 *)smem;                                       // [MT][KSM] X', pair order of the encoding
+  f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [MT][KSM / UK] (Xlo, Xhi) per unit
+  float *sR = (float *)smem;                                   // after the stream: partials
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ch = wave / GV_SUB, sub = wave % GV_SUB;
-  const uint32_t nB = blockIdx.x * 128u;
+  const int ch = wave / GV_KSUB, sub = wave % GV_KSUB;
+  const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
+  const uint32_t nB = tile * 128u, kb0 = slice * KS;
   const uint32_t r = wrow(p, nB + ch * 64 + lane);
+  const uint32_t nuw = KS / UK / GV_KSUB;                      // units of this wave
+  const uint32_t u0 = sub * nuw;                               // its first unit inside the slice
 
-  auto load = [&](Unit<WE> &u, uint32_t k) {
-    const uint32_t kc = p.wk0 + k;
+  // byte offset of this lane's first unit from the tensor start: 32-bit (the host routes tensors of 4 GiB or more to
+  // the MFMA kernel), so every load is the uniform base plus one per-lane offset, advanced by a constant per unit
+  uint32_t woff;
+  if constexpr (WE == W_Q4) woff = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5)) * 1280u + (r & 63u) * 16u;
+  else if constexpr (WE == W_Q8) woff = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 6)) * 4224u + (r & 63u) * 64u;
+  else woff = (r * p.wG + p.wk0 + kb0) * 2u;
+  constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
+
+  auto load = [&](Unit<WE> &u, uint32_t unit) {
+    const uint8_t *src = p.W + (woff + unit * USTRIDE);
     if constexpr (WE == W_Q4) {
-      const uint8_t *rec = p.W + ((size_t)(r >> 6) * p.wG + (kc >> 5)) * 1280u;
-      u.code = *(const u32x4 *)(rec + (r & 63u) * 16u);
-      u.sm = *(const uint32_t *)(rec + 1024u + (r & 63u) * 4u);
+      u.code = __builtin_nontemporal_load((const u32x4 *)src);
+      u.sm = __builtin_nontemporal_load((const uint32_t *)(src + 1024u - (r & 63u) * 12u));   // scale word r
     } else if constexpr (WE == W_Q8) {
-      const uint8_t *rec = p.W + ((size_t)(r >> 6) * p.wG + (kc >> 6)) * 4224u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) u.code[i] = *(const u32x4 *)(rec + (r & 63u) * 64u + 16u * i);
-      u.s = *(const uint32_t *)(rec + 4096u + (r & 62u) * 2u);
+      for (int i = 0; i < 4; i++) u.code[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16u * i));
+      u.s = __builtin_nontemporal_load((const uint32_t *)(src + 4096u - (r & 63u) * 64u + (r & 62u) * 2u));
     } else {
-      const uint8_t *src = p.W + ((size_t)r * p.wG + kc) * 2;
-      if (p.flags & F_WALIGN8) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) u.v[i] = *(const u32x4 *)(src + 16 * i);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          u32x2 lo = *(const u32x2 *)(src + 16 * i), hi = *(const u32x2 *)(src + 16 * i + 8);
-          u.v[i] = (u32x4){lo.x, lo.y, hi.x, hi.y};
-        }
-      }
+      for (int i = 0; i < 4; i++) u.v[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16 * i));
     }
   };
+
+  // the nibble masks and the fp16 exponent in registers, so each pair is one v_and_or_b32 (gfx9 VOP3 takes no
+  // literal operands)
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mag = 0x64006400u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi), "+v"(mag));
 
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; m++) acc[m] = 0.0f;
 
-  auto compute = [&](const Unit<WE> &u, int ku) {      // ku: the unit's k offset inside the chunk
-    f16x2 w[UK / 2];
+  auto compute = [&](const Unit<WE> &u, uint32_t unit) {
+    const f16 *xs = sX + unit * UK;
     if constexpr (WE == W_Q4) {
-      bool fast = q4_fast_ok(u.sm);
-      dq_q4_word(u.code.x, u.sm, fast, w + 0);
-      dq_q4_word(u.code.y, u.sm, fast, w + 4);
-      dq_q4_word(u.code.z, u.sm, fast, w + 8);
-      dq_q4_word(u.code.w, u.sm, fast, w + 12);
-    } else if constexpr (WE == W_Q8) {
-      uint32_t sh = (r & 1u) ? (u.s >> 16) : (u.s & 0xffffu);
-      f16x2 s2 = as_h2(sh | (sh << 16));
+      const uint32_t wd[4] = {u.code.x, u.code.y, u.code.z, u.code.w};
+      uint32_t h[16];                                           // per word: (q0,q4) (16q1,16q5) (q2,q6) (16q3,16q7)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        dq_q8_word(u.code[i].x, s2, w + 8 * i + 0);
-        dq_q8_word(u.code[i].y, s2, w + 8 * i + 2);
-        dq_q8_word(u.code[i].z, s2, w + 8 * i + 4);
-        dq_q8_word(u.code[i].w, s2, w + 8 * i + 6);
+        const uint32_t w8 = wd[i] >> 8;
+        h[4 * i + 0] = (wd[i] & mlo) | mag;
+        h[4 * i + 1] = (wd[i] & mhi) | mag;
+        h[4 * i + 2] = (w8 & mlo) | mag;
+        h[4 * i + 3] = (w8 & mhi) | mag;
+      }
+      const f16x2 sm2 = as_h2(u.sm);
+      const float s = (float)sm2.x, mn = (float)sm2.y;
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const u32x4 *x4 = (const u32x4 *)(xs + m * KSM);
+        float dlo = 0.0f, dhi = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 xv = x4[i];
+          dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), dlo, false);
+          dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), dhi, false);
+          dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), dlo, false);
+          dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), dhi, false);
+        }
+        const f32x2 g = sG[m * NGM + unit];
+        const float t = fmaf(-1024.0f, g.x, dlo) + 0.0625f * fmaf(-1024.0f, g.y, dhi);   // sum x q, exact for e_k
+        acc[m] = fmaf(s, t, fmaf(mn, g.x + g.y, acc[m]));
+      }
+    } else if constexpr (WE == W_Q8) {
+      uint32_t h[32];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t wd[4] = {u.code[i].x ^ 0x80808080u, u.code[i].y ^ 0x80808080u, u.code[i].z ^ 0x80808080u,
+                                u.code[i].w ^ 0x80808080u};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          h[8 * i + 2 * j + 0] = perm(0x64646464u, wd[j], 0x04020400u);   // (1152 + q0, 1152 + q2)
+          h[8 * i + 2 * j + 1] = perm(0x64646464u, wd[j], 0x04030401u);   // (1152 + q1, 1152 + q3)
+        }
+      }
+      const uint32_t sh = (r & 1u) ? (u.s >> 16) : (u.s & 0xffffu);
+      const float s = (float)__builtin_bit_cast(f16, (uint16_t)sh);
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const u32x4 *x4 = (const u32x4 *)(xs + m * KSM);
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const u32x4 xv = x4[i];
+          d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), d, false);
+          d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), d, false);
+          d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), d, false);
+          d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), d, false);
+        }
+        const f32x2 g = sG[m * NGM + unit];
+        acc[m] = fmaf(s, fmaf(-1152.0f, g.x + g.y, d), acc[m]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        w[4 * i + 0] = as_h2(u.v[i].x); w[4 * i + 1] = as_h2(u.v[i].y);
-        w[4 * i + 2] = as_h2(u.v[i].z); w[4 * i + 3] = as_h2(u.v[i].w);
+      for (int m = 0; m < MT; m++) {
+        const u32x4 *x4 = (const u32x4 *)(xs + m * KSM);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 xv = x4[i];
+          acc[m] = __builtin_amdgcn_fdot2(as_h2(u.v[i].x), as_h2(xv.x), acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(as_h2(u.v[i].y), as_h2(xv.y), acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(as_h2(u.v[i].z), as_h2(xv.z), acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(as_h2(u.v[i].w), as_h2(xv.w), acc[m], false);
+        }
       }
     }
+  };
+
+  // fill the ring before X' is staged, so HBM works while the prologue runs
+  Unit<WE> ring[PF];
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-      const u32x4 *xs = (const u32x4 *)(sX + m * GV_KC + ku);
+  for (int j = 0; j < PF; j++)
+    if ((uint32_t)j < nuw) load(ring[j], u0 + j);
+
+  // X' of the slice -> LDS in the pair order of the encoding; then per unit the X' sums over the low (even pair slot)
+  // and high (odd pair slot) positions
+  const uint32_t nb = KS / 8, ng = KS / UK;
+  for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
+    uint32_t m = t / nb, kq = t - m * nb;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (m < p.M) v = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq));
+    *(u32x4 *)(sX + m * KSM + 8 * kq) = v;
+  }
+  if constexpr (WE != W_F16) {
+    __syncthreads();
+    for (uint32_t t = tid; t < MT * ng; t += GV_NT) {
+      uint32_t m = t / ng, g = t - m * ng;
+      const u32x4 *x4 = (const u32x4 *)(sX + m * KSM + g * UK);
+      float lo = 0.0f, hi = 0.0f;
 #pragma unroll
       for (int q = 0; q < UK / 8; q++) {
-        u32x4 xv = xs[q];
-        acc[m] = __builtin_amdgcn_fdot2(w[4 * q + 0], as_h2(xv.x), acc[m], false);
-        acc[m] = __builtin_amdgcn_fdot2(w[4 * q + 1], as_h2(xv.y), acc[m], false);
-        acc[m] = __builtin_amdgcn_fdot2(w[4 * q + 2], as_h2(xv.z), acc[m], false);
-        acc[m] = __builtin_amdgcn_fdot2(w[4 * q + 3], as_h2(xv.w), acc[m], false);
+        const u32x4 xv = x4[q];
+        const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
+        lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
+        hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
       }
+      sG[m * NGM + g] = (f32x2){lo, hi};
     }
-  };
-
-  Unit<WE> cur[UPW], nxt[UPW];
-  const uint32_t K = p.K;
-  auto load_chunk = [&](Unit<WE> *dst, uint32_t kc0) {
-    uint32_t nu = (K - kc0 < (uint32_t)GV_KC ? K - kc0 : (uint32_t)GV_KC) / UK;
-#pragma unroll
-    for (int j = 0; j < UPW; j++) {
-      uint32_t u = sub + GV_SUB * j;
-      if (u < nu) load(dst[j], kc0 + u * UK);
-    }
-  };
-
-  load_chunk(cur, 0);
-  for (uint32_t kc0 = 0; kc0 < K; kc0 += GV_KC) {
-    const uint32_t kn = K - kc0 < (uint32_t)GV_KC ? K - kc0 : (uint32_t)GV_KC;
-    // X' of this chunk -> LDS
-    const uint32_t nb = kn / 8;
-    for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
-      uint32_t m = t / nb, kb = t - m * nb;
-      u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-      if (m < p.M) v = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kc0 + 8 * kb));
-      *(u32x4 *)(sX + m * GV_KC + 8 * kb) = v;
-    }
-    __syncthreads();
-    if (kc0 + GV_KC < K) load_chunk(nxt, kc0 + GV_KC);
-    const uint32_t nu = kn / UK;
-#pragma unroll
-    for (int j = 0; j < UPW; j++) {
-      uint32_t u = sub + GV_SUB * j;
-      if (u < nu) compute(cur[j], u * UK);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < UPW; j++) cur[j] = nxt[j];
   }
+  __syncthreads();
 
-  // the 4 K-slices meet in LDS
+  // the stream: reduce slot j, refill it with the unit PF ahead
+  uint32_t j0 = 0;
+#pragma unroll 1
+  for (; j0 + PF <= nuw; j0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      compute(ring[j], u0 + j0 + j);
+      // refill unconditionally (past the end: the wave's last unit again, unused): a conditional refill would keep
+      // the old and the new slot contents apart and double the ring's registers
+      const uint32_t nx = j0 + PF + j;
+      load(ring[j], u0 + (nx < nuw ? nx : nuw - 1u));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PF; j++)
+    if (j0 + j < nuw) compute(ring[j], u0 + j0 + j);
+  __syncthreads();                                             // X' is dead: the buffer takes the partials
+
+  // the K-quarters meet in LDS
 #pragma unroll
   for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + ch * 64 + lane] = acc[m];
   __syncthreads();
   for (int t = tid; t < MT * 128; t += GV_NT) {
     float s = sR[t];
 #pragma unroll
-    for (int q = 1; q < GV_SUB; q++) s += sR[q * MT * 128 + t];
+    for (int q = 1; q < GV_KSUB; q++) s += sR[q * MT * 128 + t];
     sR[t] = s;
   }
   __syncthreads();
+
+  if (S > 1) {
+    // partial tile -> workspace [slice][m][ws column, padded to whole tiles]. The partials, the counter and the reads
+    // of the last item all go to the memory side (system-coherent accesses that skip the per-XCD L2s), so items on
+    // different XCDs meet without any L2 writeback or invalidation: a store is acknowledged only once it is there,
+    // and every thread waits for its acknowledgements before the barrier that precedes the counter update.
+    const uint32_t Np = gridDim.x / S * 128u;
+    const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+      uint32_t m = t >> 7, c = t & 127;
+      __hip_atomic_store(part + ((size_t)slice * p.M + m) * Np + nB + c, sR[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t old = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sLast = (old == S - 1u) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+      uint32_t m = t >> 7, c = t & 127;
+      const float *src = part + (size_t)m * Np + nB + c;
+      float s = 0.0f;
+      for (uint32_t q = 0; q < S; q++)
+        s += __hip_atomic_load(src + (size_t)q * p.M * Np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sR[t] = s;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+  }
   epilogue<GV_NT>(p, sR, 128, MT, 0u, nB, tid);
 }
 
+static uint32_t ks_max_of(uint32_t M) {
+  return M <= 1 ? ks_max<1>() : M <= 2 ? ks_max<2>() : M <= 4 ? ks_max<4>() : M <= 8 ? ks_max<8>() : ks_max<16>();
+}
+
+// Slices per tile: the fewest that fill the GPU with items (about one per CU) and keep each slice's X' inside the LDS
+// budget, with a whole number of units per K-quarter.
+void gemv_split(const Params &p, int we, unsigned cus, unsigned *S_out, unsigned *KS_out) {
+  const uint32_t tiles = (p.N + 127) / 128;
+  const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;     // k per "one unit in each K-quarter"
+  const uint32_t ksm = ks_max_of(p.M);
+  uint32_t S = 1;
+  while ((tiles * S < cus * 7u / 8u || p.K / S > ksm) && p.K % (2u * S * quant) == 0) S *= 2u;
+  if (p.K % (S * quant) != 0 || p.K / S > ksm) S = 0;             // caller falls back to the MFMA kernel
+  *S_out = S;
+  *KS_out = S ? p.K / S : 0;
+}
+
 template <int WE, int XM, int MT>
-static hipError_t launch3(const Params &p, hipStream_t s) {
-  dim3 grid((p.N + 127) / 128);
-  hipLaunchKernelGGL((k_gemv<WE, XM, MT>), grid, dim3(GV_NT), 0, s, p);
+static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
+  if (KS > (uint32_t)ks_max<MT>()) return hipErrorInvalidValue;
+  dim3 grid(((p.N + 127) / 128) * S);
+  hipLaunchKernelGGL((k_gemv<WE, XM, MT>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
   return hipGetLastError();
 }
 template <int WE, int XM>
-static hipError_t launch2(const Params &p, hipStream_t s) {
-  if (p.M <= 1) return launch3<WE, XM, 1>(p, s);
-  if (p.M <= 2) return launch3<WE, XM, 2>(p, s);
-  if (p.M <= 4) return launch3<WE, XM, 4>(p, s);
-  if (p.M <= 8) return launch3<WE, XM, 8>(p, s);
-  return launch3<WE, XM, 16>(p, s);
+static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
+  if (p.M <= 1) return launch3<WE, XM, 1>(p, part, cnt, S, KS, s);
+  if (p.M <= 2) return launch3<WE, XM, 2>(p, part, cnt, S, KS, s);
+  if (p.M <= 4) return launch3<WE, XM, 4>(p, part, cnt, S, KS, s);
+  if (p.M <= 8) return launch3<WE, XM, 8>(p, part, cnt, S, KS, s);
+  return launch3<WE, XM, 16>(p, part, cnt, S, KS, s);
 }
 template <int WE>
-static hipError_t launch1(const Params &p, int xm, hipStream_t s) {
+static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
   switch (xm) {
-  case X_F16: return launch2<WE, X_F16>(p, s);
-  case X_LNMOD: return launch2<WE, X_LNMOD>(p, s);
-  case X_RMS: return launch2<WE, X_RMS>(p, s);
+  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s);
+  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s);
+  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(const Params &p, int we, int xm, hipStream_t s) {
-  if (p.M > (uint32_t)GEMV_MAX_M) return hipErrorInvalidValue;
+hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
+                       hipStream_t s) {
+  const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
+  if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
   switch (we) {
-  case W_Q4: return launch1<W_Q4>(p, xm, s);
-  case W_Q8: return launch1<W_Q8>(p, xm, s);
-  case W_F16: return launch1<W_F16>(p, xm, s);
+  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s);
+  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s);
+  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s);
   }
   return hipErrorInvalidValue;
 }

@@ -7,7 +7,8 @@
 namespace p0k {
 struct Params;
 enum { K_MFMA = 0, K_GEMV = 1 };
-struct Plan { int kernel, we, xm; unsigned bm, bn; };
+// kernel choice of one call: GEMV items are (128-column tile) x (K slice of KS), S slices per tile
+struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; };
 // validate a gemm call and translate it to kernel parameters (device pointers are filled in by the caller)
 int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err);
 int prepare_rowstats(const p0k_rowstats_args *a, std::string *err);

@@ -4,12 +4,15 @@
 
 namespace p0k {
 struct Params;
+constexpr int GEMV_MAX_M = 16;
+constexpr unsigned MI355X_CUS = 256;
 // MFMA GEMM (any M): 128 x 128 tiles, 256 threads
 hipError_t launch_gemm_mfma(const Params &p, int we, int xm, hipStream_t s);
-// decode GEMV (M <= 16, prologue f16 / rms / lnmod): 128 ws columns per workgroup, 512 threads
-hipError_t launch_gemv(const Params &p, int we, int xm, hipStream_t s);
+// decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
+// (part: S*M*N floats, cnt: one zeroed counter per 128-column tile)
+void gemv_split(const Params &p, int we, unsigned cus, unsigned *S, unsigned *KS);
+hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s);
 // rowstats (src/ops/misc.js:16-44)
-hipError_t launch_rowstats(const void *x, uint32_t ld, uint32_t c0, uint32_t rows, uint32_t cols, int mode, float eps,
-                           float *st, uint32_t st_off, hipStream_t s);
-constexpr int GEMV_MAX_M = 16;
+hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
+                           float *st, unsigned st_off, hipStream_t s);
 }  // namespace p0k

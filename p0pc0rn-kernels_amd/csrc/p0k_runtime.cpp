@@ -50,6 +50,12 @@ struct p0k_ctx {
   uint64_t alive = 0, peak = 0, pooled = 0, hw = 0, max_buf = 0, seq = 0;
   uint64_t creates = 0, reuses = 0, evictions = 0, pooled_n = 0;
   uint64_t cap() const { return hw + max_buf; }
+  // workspace of the split-K decode GEMV: fp32 partial tiles (grown on demand) and one arrival counter per 128-column
+  // tile (zeroed once here; every call leaves them at zero again)
+  float *ws_part = nullptr;
+  uint64_t ws_part_bytes = 0;
+  uint32_t *ws_cnt = nullptr;
+  static constexpr uint32_t WS_COUNTERS = 1u << 16;
 };
 
 struct p0k_event { hipEvent_t ev; int device; };
@@ -74,6 +80,9 @@ int p0k_ctx_create(int device, p0k_ctx **out) {
   c->device = device;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) { delete c; return hip_err(e, "hipStreamCreate"); }
+  e = hipMalloc((void **)&c->ws_cnt, sizeof(uint32_t) * p0k_ctx::WS_COUNTERS);
+  if (e == hipSuccess) e = hipMemset(c->ws_cnt, 0, sizeof(uint32_t) * p0k_ctx::WS_COUNTERS);
+  if (e != hipSuccess) { (void)hipStreamDestroy(c->stream); delete c; return hip_err(e, "workspace counters"); }
   *out = c;
   return P0K_OK;
 }
@@ -85,6 +94,8 @@ void p0k_ctx_destroy(p0k_ctx *c) {
   for (auto &kv : c->live) (void)hipFree(kv.first);
   for (auto &kv : c->pool)
     for (auto &b : kv.second) (void)hipFree(b.ptr);
+  if (c->ws_part) (void)hipFree(c->ws_part);
+  if (c->ws_cnt) (void)hipFree(c->ws_cnt);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -301,8 +312,32 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   p.ST = a->st_buf; p.PV = a->pv_buf; p.EV = a->ev_buf; p.BV = a->bv_buf; p.RP = a->rope_buf;
   p.GT = (const uint16_t *)a->gt_buf;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = plan.kernel == p0k::K_GEMV ? p0k::launch_gemv(p, plan.we, plan.xm, c->stream)
-                                             : p0k::launch_gemm_mfma(p, plan.we, plan.xm, c->stream);
+  hipError_t e;
+  if (plan.kernel == p0k::K_GEMV) {
+    const uint32_t tiles = (a->N + 127) / 128;
+    if (plan.S > 1) {
+      if (tiles > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "gemm: N too large for the decode workspace");
+      const uint64_t need = (uint64_t)plan.S * a->M * tiles * 128u * sizeof(float);
+      std::lock_guard<std::mutex> lk(c->mu);
+      if (need > c->ws_part_bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIPCHK(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+          return set_err(P0K_E_ARG, "gemm: the decode workspace must grow (" + std::to_string(need) +
+                                        " bytes): make one call of this shape before capturing a graph");
+        HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        if (c->ws_part) HIPCHK(hipFree(c->ws_part), "hipFree");
+        c->ws_part = nullptr;
+        c->ws_part_bytes = 0;
+        hipError_t me = hipMalloc((void **)&c->ws_part, need);
+        if (me != hipSuccess) return set_err(P0K_E_NOMEM, "gemm: workspace of " + std::to_string(need) + " bytes");
+        c->ws_part_bytes = need;
+      }
+    }
+    e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream);
+  } else {
+    e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, c->stream);
+  }
   if (e != hipSuccess) return hip_err(e, "gemm launch");
   return P0K_OK;
 }

@@ -66,9 +66,16 @@ class Case:
     def host_copy(self):
         return {k: v.copy() for k, v in self.bufs.items()}
 
-    def run_oracle(self, m0=0, m1=None):
+    def run_oracle(self, m0=0, m1=None, weights=None):
+        """weights: the oracle's weight model; by default the one the HIP kernel for this call computes with (the
+        decode GEMV sums over fp32 dequantised weights like the reference's cpuGemm, the MFMA GEMM over fp16 ones
+        like the reference's kernel)."""
         h = self.host_copy()
-        oracle.gemm(self.args(lambda n: h[n]), m0, m1)
+        a = self.args(lambda n: h[n])
+        if weights is None:
+            import p0k
+            weights = oracle.CPU_WEIGHTS if p0k.select_tile(a)["kernel"] == "gemv" else oracle.KERNEL_WEIGHTS
+        oracle.gemm(a, m0, m1, weights)
         return h[self.out]
 
     def run_device(self, dev, upload=None):

@@ -9,6 +9,7 @@ import subprocess
 import numpy as np
 import pytest
 
+import oracle
 import p0k
 from cases import assert_close, make_case, make_conv3_case
 
@@ -40,13 +41,13 @@ def run_js(case, tmp_path):
 def test_js_port_matches_oracle(kw, tmp_path):
     case = make_case(seed=4, **kw)
     got = run_js(case, tmp_path)
-    want = case.run_oracle()
+    want = case.run_oracle(weights=oracle.CPU_WEIGHTS)          # both restate cpuGemm's fp32 dequantised weights
     assert_close(got, want, fp16=want.dtype == np.uint16, what="cpu_ref.mjs vs oracle")
 
 
 def test_js_port_conv3_matches_oracle(tmp_path):
     case = make_conv3_case(T=3, H=4, W=5, C=32, N=64, pn=True)
-    assert_close(run_js(case, tmp_path), case.run_oracle(), what="cpu_ref.mjs conv3")
+    assert_close(run_js(case, tmp_path), case.run_oracle(weights=oracle.CPU_WEIGHTS), what="cpu_ref.mjs conv3")
 
 
 def test_js_bench_runs():

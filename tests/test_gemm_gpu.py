@@ -117,7 +117,7 @@ def test_dequant_bit_exact(dev, enc, path):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
     to exercise both decoder paths."""
-    rows, K = 128, 128
+    rows, K = 128, 256
     wb = _adversarial_q4(rows, K, 3) if enc.startswith("q4") else _adversarial_q8(rows, K, 4)
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
     dw = dev.upload(wb)

@@ -146,12 +146,26 @@ CASES = [
 @pytest.mark.parametrize("kw", CASES, ids=lambda k: f"{k['enc']}-{k.get('xmode', 'f16')}-{k['epi']}")
 def test_oracle_gemm_against_numpy(kw):
     case = make_case(seed=3, **kw)
-    got = case.run_oracle()
+    got = case.run_oracle(weights=oracle.KERNEL_WEIGHTS)
     want = epi_numpy(case, acc_numpy(case))
     fp16 = got.dtype == np.uint16
     assert_close(got, want, fp16=fp16, what="oracle vs numpy")
     if fp16:   # same rounding points and float64 sums: almost every value is bit-identical
         assert np.mean(got == want) > 0.995
+
+
+@pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
+def test_oracle_cpu_weight_model_is_cpuGemm(enc):
+    """CPU_WEIGHTS: y = X W^T over the encoders' fp32 dequantised weights, exactly the test suite's cpuGemm
+    (test/kernels.test.js:25-29, float64 sums), rounded once to fp32."""
+    M, N, K = 8, 128, 256
+    X = oracle.h2f(oracle.f16_bits(oracle.randn(M * K, 7)))
+    W0 = oracle.randn(N * K, 11, 0.05)
+    wb, deq = (oracle.pack_q4 if enc.startswith("q4") else oracle.pack_q8)(W0, N, K, want_deq=True)
+    y = np.zeros(M * N, np.float32)
+    oracle.gemm({"w": {"enc": enc, "buf": wb, "rows": N, "cols": K}, "x": {"buf": oracle.f16_bits(X)}, "y": {"buf": y},
+                 "M": M, "N": N, "K": K, "epi": "f32"}, weights=oracle.CPU_WEIGHTS)
+    assert np.array_equal(y, oracle.cpu_gemm(X, deq, M, N, K))
 
 
 def test_oracle_plain_gemm_is_cpuGemm():
@@ -235,7 +249,7 @@ def test_rope_2d_table_closed_form():
 def test_heads_invariants():
     """RoPE is a rotation: per pair, |v| is the same before and after; V heads pass through un-normalised."""
     case = make_case(enc="f16", epi="heads", M=6, N=384, K=64, seed=9, Hq=1, Hkv=1, rope_mode="half")
-    got = oracle.h2f(case.run_oracle()).reshape(3, -1, 128).astype(np.float64)
+    got = oracle.h2f(case.run_oracle(weights=oracle.KERNEL_WEIGHTS)).reshape(3, -1, 128).astype(np.float64)
     acc = acc_numpy(case)
     v = got[2, :6]
     assert np.allclose(v, f16r(acc[:, 256:384]), atol=0, rtol=0)
