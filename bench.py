@@ -15,7 +15,13 @@ fixed seeds, encoded with libp0k's own FORMAT.md encoders (BASELINE.json value r
 
 cpu_baseline: the build's JavaScript restatement of the reference's CPU path (cpuGemm, float64 sums over dequantised
 fp32 weights, with the same prologue / epilogue formulas; oracle/cpu_ref.mjs) timed in Node on this host, one core,
-on a bounded row sample of the same workload, scaled linearly in M (the cost is exactly linear in M).
+on a bounded sample: for the headline, whole M = 1 calls repeated for about 10 s; for the other workloads one call's
+weight decode plus a few rows of M, scaled linearly in M (the cost is exactly linear in M).
+
+    python bench.py --copy-calib
+
+runs only a plain device-to-device copy of 1 GiB, 5 times (torch's copy kernel): the reference workload for scaling the
+FETCH_SIZE / WRITE_SIZE counters of rocprofv3 into bytes (what they read for a copy of known size).
 """
 import argparse
 import json
@@ -235,13 +241,15 @@ def roofline(wl, ms):
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(config, rows):
-    """Run the JavaScript CPU restatement in Node on a row sample; returns its JSON report or None."""
+def cpu_baseline(config, rows, target_s=0.0):
+    """Run the JavaScript CPU restatement in Node: one call over `rows` rows of M, repeated for about target_s seconds
+    when target_s > 0; returns its JSON report or None."""
     script = os.path.join(ROOT, "oracle", "cpu_ref.mjs")
     if not os.path.exists(script):
         return None
     try:
-        out = subprocess.run(["node", script, "bench", config, str(rows)], capture_output=True, text=True, timeout=240)
+        out = subprocess.run(["node", script, "bench", config, str(rows), str(target_s)], capture_output=True,
+                             text=True, timeout=240)
     except (OSError, subprocess.TimeoutExpired) as e:
         log(f"cpu baseline {config}: {e}")
         return None
@@ -251,11 +259,23 @@ def cpu_baseline(config, rows):
     return json.loads(out.stdout.strip().splitlines()[-1])
 
 
+CPU_HEADLINE_S = 10.0   # seconds of CPU work timed for the headline workload (whole calls, repeated)
 CPU_SAMPLE = {   # workload -> (cpu_ref config, rows of M timed)
     "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 1), "decode_q4_swiglu_M16": ("decode", 1),
     "prefill_q8_rms_resadd": ("prefill", 1), "dit_qkv_q4_lnmod_heads": ("dit_qkv", 1), "dit_up_q4_geglu": ("dit_up", 1),
     "conv3_128_T13x92x160": ("conv3", 64),
 }
+
+
+def copy_calib(nbytes=1 << 30, reps=5):
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}), flush=True)
 
 
 def main():
@@ -265,11 +285,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (the gemm path has no multi-GPU mode here); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
+    if a.copy_calib:
+        copy_calib()
+        return
     names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
     dev = p0k.Device(0)
     info = dev.info()
@@ -293,21 +317,27 @@ def main():
         cache = {}
         for n, res in results.items():
             cfg, rows = CPU_SAMPLE[res["name"]]
-            if (cfg, rows) not in cache:
-                cache[(cfg, rows)] = cpu_baseline(cfg, rows)
-            cb = cache[(cfg, rows)]
+            whole = n == "decode1"                                       # the headline: time whole M=1 calls
+            key = (cfg, rows, whole)
+            if key not in cache:
+                cache[key] = cpu_baseline(cfg, rows, CPU_HEADLINE_S if whole else 0.0)
+            cb = cache[key]
             if cb:
-                cpu_ms = cb["deq_ms"] + cb["ms_per_row"] * res["M"]      # decode the weights once, then M rows
-                res["cpu"] = {"ms_per_call": cpu_ms, "sample_rows": cb["rows"], "sample_ms": cb["ms"],
-                              "node": cb.get("node"), "cpu_model": cb.get("cpu")}
+                if whole:
+                    cpu_ms = cb["ms_per_call"]
+                    sample = f"{cb['calls']} whole calls of this workload in {cb['ms'] / 1e3:.1f} s"
+                else:
+                    cpu_ms = cb["deq_ms"] + cb["ms_per_row"] * res["M"]  # decode the weights once, then M rows
+                    sample = f"{cb['rows']} row(s) of M in {cb['ms']:.0f} ms, scaled to M rows"
+                res["cpu"] = {"ms_per_call": cpu_ms, "sample": sample, "node": cb.get("node"),
+                              "cpu_model": cb.get("cpu"), "host_cores": cb.get("host_cores")}
                 res["x_vs_cpu"] = round(cpu_ms / res["ms_per_call"], 1)
-                log(f"cpu {res['name']}: {cpu_ms:.1f} ms/call (sample {cb['rows']} rows in {cb['ms']:.0f} ms) "
-                    f"-> x{res['x_vs_cpu']}")
+                log(f"cpu {res['name']}: {cpu_ms:.1f} ms/call ({sample}) -> x{res['x_vs_cpu']}")
     head = results.get("decode1") or next(iter(results.values()))
     hw = {k: v for k, v in head.items() if k not in ("roofline", "cpu")}
     cpu = head.get("cpu")
     line = {
-        "metric": "q4 GEMV decode + SwiGLU, HBM GB/s of algorithmic bytes (M=1, out 14336, K=4096)",
+        "metric": "q4/q8 GEMM TFLOP/s + HBM GB/s (% roofline) at M=1 and M=4096; x vs CPU ref",
         "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": head["calls"], "warmup": a.warmup,
         "ms_per_step": head["ms_per_call"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4 weights (u4 codes -> fp16), fp16 activations, fp32 accumulate", "data": "synthetic (seeded PCG64)",
@@ -316,8 +346,8 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": ({"value": round(head["algo_bytes"] / (cpu["ms_per_call"] * 1e6), 3), "unit": "GB/s",
                           "cores": cores, "kind": "port",
-                          "sample": f"{cpu['sample_rows']} row(s) of M in {cpu['sample_ms']:.0f} ms, Node {cpu['node']}, "
-                                    f"{cpu['cpu_model']}, scaled x M"} if cpu else None),
+                          "sample": f"{cpu['sample']}; oracle/cpu_ref.mjs on Node {cpu['node']}, one thread of "
+                                    f"{cpu['host_cores']} host cores ({cpu['cpu_model']})"} if cpu else None),
         "device": info["name"],
         "workloads": list(results.values()),
         "wall_ms_per_step": round(hw.get("ms_per_call", 0), 5),

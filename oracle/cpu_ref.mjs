@@ -203,7 +203,7 @@ const CONFIGS = {   // BASELINE.json configs, as (args, buffers) for the given n
       { w: bytesOf(randnF16(N * K, 11).map((h) => f2h(0.02 * H2F[h]))), x: bytesOf(randnF16(T * H * W * C, 12)), y: new Uint8Array(M * N * 2) }]; },
 };
 
-function bench(config, rows) {
+function bench(config, rows, targetS) {
   const [a, b] = CONFIGS[config](rows);
   const t0 = process.hrtime.bigint();
   const Wd = gemmRows(a, b, 0, 1);                       // the weights are decoded once per call, then row 0
@@ -215,8 +215,17 @@ function bench(config, rows) {
   if (rows > 1) rowMs = Number(t2 - t1) / 1e6 / (rows - 1);
   else { const t3 = process.hrtime.bigint(); gemmRows(a, b, 0, 1, Wd); rowMs = Number(process.hrtime.bigint() - t3) / 1e6; }
   const firstMs = Number(t1 - t0) / 1e6;
+  // whole calls (decode + every row) repeated until targetS seconds have passed: the timed sample
+  let calls = 1, totalMs = firstMs + Number(t2 - t1) / 1e6;
+  const t4 = process.hrtime.bigint();
+  while (targetS > 0 && Number(process.hrtime.bigint() - t4) / 1e9 + totalMs / 1e3 < targetS) {
+    const d = gemmRows(a, b, 0, 1);
+    gemmRows(a, b, 1, rows, d);
+    calls++;
+  }
+  if (calls > 1) totalMs += Number(process.hrtime.bigint() - t4) / 1e6;
   const cpus = os.cpus();
-  console.log(JSON.stringify({ config, rows, ms: firstMs + Number(t2 - t1) / 1e6, deq_ms: Math.max(0, firstMs - rowMs),
+  console.log(JSON.stringify({ config, rows, ms: totalMs, calls, ms_per_call: totalMs / calls, deq_ms: Math.max(0, firstMs - rowMs),
     ms_per_row: rowMs, node: process.version, cpu: cpus.length ? cpus[0].model : '?', host_cores: cpus.length }));
 }
 
@@ -228,5 +237,5 @@ function check(dir) {
   fs.writeFileSync(path.join(dir, 'y_js.bin'), b.y);
 }
 
-if (process.argv[2] === 'bench') bench(process.argv[3], parseInt(process.argv[4] || '1', 10));
+if (process.argv[2] === 'bench') bench(process.argv[3], parseInt(process.argv[4] || '1', 10), parseFloat(process.argv[5] || '0'));
 else if (process.argv[2] === 'check') check(process.argv[3]);

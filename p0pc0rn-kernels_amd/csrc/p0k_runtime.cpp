@@ -106,6 +106,9 @@ int p0k_device_info_get(p0k_ctx *c, p0k_device_info *out) {
   HIPCHK(hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties");
   memset(out, 0, sizeof *out);
   snprintf(out->name, sizeof out->name, "%s", prop.name);
+  if (!out->name[0])   // some drivers report no marketing name: name the device by its ISA and size instead
+    snprintf(out->name, sizeof out->name, "AMD %.16s, %d CUs, %zu GiB", prop.gcnArchName, prop.multiProcessorCount,
+             (size_t)(prop.totalGlobalMem >> 30));
   snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
   out->cus = prop.multiProcessorCount;
   out->xcds_hint = 8;

@@ -1,0 +1,151 @@
+"""The Node N-API addon and JavaScript shim (p0pc0rn-kernels_amd/node/index.mjs) that keep the reference's JavaScript
+API: createGpu / upload / read / free (src/core/gpu.js), gemm(gpu, args) (src/ops/gemm.js:268), loadWeights
+(src/weights.js:10), f2h / h2f (src/core/gpu.js:276-299), packQ4 / packQ8 / packF16 (src/convert/encode.js:56-98).
+
+The host tests need no GPU; the gpu tests run reference-style argument objects through the shim and compare the output
+with the oracle at the same tolerance as the C-ABI tests."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from cases import assert_close, make_case, make_conv3_case
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NODE = shutil.which("node")
+DRIVER = os.path.join(ROOT, "tests", "node", "run_case.mjs")
+ADDON = os.path.join(ROOT, "p0pc0rn-kernels_amd", "node", "p0k.node")
+pytestmark = [pytest.mark.skipif(NODE is None, reason="node is not installed"),
+              pytest.mark.skipif(not os.path.exists(ADDON), reason="p0k.node is not built")]
+
+
+def node(mode, d, timeout=120):
+    r = subprocess.run([NODE, DRIVER, mode, str(d)], capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr[-3000:]
+
+
+def test_host_helpers_and_errors(tmp_path):
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([rng.standard_normal(4000).astype(np.float32) * np.float32(2.0) ** rng.integers(-30, 18, 4000),
+                           np.array([0, -0.0, 65504, 65520, 65519.99, 1e-8, -2 ** -24, 2 ** -25, 3 * 2 ** -26, np.inf, -np.inf,
+                                     np.nan, 6.1e-5, 6.0e-5, 1e5], np.float32)]).astype(np.float32)
+    vals.tofile(str(tmp_path / "values.f32"))
+    f64 = [0.1, 1 / 3, 65519.0, 2.0 ** -24 * 1.5000000001, 1.0009765625 + 2 ** -12]
+    (tmp_path / "f64.json").write_text(json.dumps(f64))
+    rows, K = 128, 256
+    W = (rng.standard_normal(rows * K) * 0.05).astype(np.float32)
+    W[:64] = 0.0                                                  # an all-zero group
+    W.tofile(str(tmp_path / "W.f32"))
+    (tmp_path / "pack.json").write_text(json.dumps({"rows": rows, "K": K}))
+    node("host", tmp_path)
+
+    got = np.fromfile(str(tmp_path / "f2h.u16"), np.uint16)
+    np.testing.assert_array_equal(got, oracle.f2h(vals))
+    h2f = np.fromfile(str(tmp_path / "h2f.f32"), np.float32)
+    want = oracle.h2f(np.arange(65536, dtype=np.uint16))
+    np.testing.assert_array_equal(np.isnan(h2f), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(h2f[ok].view(np.uint32), want[ok].view(np.uint32))
+    # float64 inputs round to binary32 first, then to binary16 (the reference's helper stores into a Float32Array)
+    assert json.loads((tmp_path / "f2h64.json").read_text()) == [int(oracle.f2h(np.float32(v))[0]) for v in f64]
+
+    q4, deq = oracle.pack_q4(W, rows, K, want_deq=True)
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "q4.bin"), np.uint8), q4)
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "q4deq.f32"), np.float32), deq)
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "q8.bin"), np.uint8), oracle.pack_q8(W, rows, K))
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "f16.bin"), np.uint16), oracle.f16_bits(W))
+
+    e = json.loads((tmp_path / "errors.json").read_text())
+    assert e["encoding"]["message"] == "gemm: unsupported weight encoding q5"         # src/ops/gemm.js:271
+    assert e["kmul32"]["message"] == "gemm: K must be a multiple of 32"               # :283
+    assert e["tile"]["message"].startswith("bad tile 48x128")                         # :31
+    assert e["rms_stats"]["message"].startswith("gemm: missing binding ST")           # :313
+    assert "Ci % 32" in e["conv3_ci"]["message"]
+    assert not any(e[k]["gpuError"] for k in ("encoding", "kmul32", "tile", "rms_stats", "conv3_ci"))
+    assert e["ok"] is None and e["plan"]["kernel"] == "gemv"
+    assert e["bytes"] == [128 // 64 * 256 // 32 * 1280, 128 // 64 * 256 // 64 * 4224, 128 * 256 * 2]
+
+
+def run_shim(case, tmp_path, tune=None):
+    names = sorted(case.bufs)
+    for n in names:
+        case.bufs[n].tofile(str(tmp_path / f"{n}.bin"))
+    (tmp_path / "bufs.json").write_text(json.dumps(names))
+    (tmp_path / "spec.json").write_text(json.dumps({"args": case.spec, "out": case.out, "tune": tune}, default=int))
+    node("gemm", tmp_path)
+    out = case.bufs[case.out]
+    y = np.fromfile(str(tmp_path / f"{case.out}_gpu.bin"), out.dtype)[:out.size]
+    return y, json.loads((tmp_path / "result.json").read_text())
+
+
+SHIM_CASES = [
+    dict(enc="q4g32a.t64", epi="swiglu", M=1, N=512, K=512),
+    dict(enc="q4g32a.t64", epi="swiglu", M=70, N=512, K=256, act="gelu", bias=True),
+    dict(enc="q8g64s.t64", xmode="rms", epi="resadd", M=3, N=256, K=256, bias=True, gate=True),
+    dict(enc="q8g64s.t64", xmode="rms", epi="resadd", M=96, N=256, K=256, store=True),
+    dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=40, N=384, K=128, Hq=1, Hkv=1, rope_mode="half", row_off=3, Ltot=64),
+    dict(enc="f16", xmode="lnmod", epi="bias", M=33, N=128, K=128, res=True),
+    dict(enc="q4g32a.t64", epi="onormgate", M=20, N=128, K=128),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kw", SHIM_CASES, ids=lambda k: f"{k['enc']}-{k.get('xmode', 'f16')}-{k['epi']}-M{k['M']}")
+def test_shim_gemm_matches_oracle(kw, tmp_path):
+    print(f"shim case {kw}", flush=True)
+    case = make_case(seed=11, **kw)
+    got, res = run_shim(case, tmp_path)
+    want = case.run_oracle()
+    assert_close(got, want, fp16=want.dtype == np.uint16, what="node shim vs oracle")
+    assert res["flops"] == 2 * kw["M"] * kw["N"] * kw["K"]
+    assert res["info"]["architecture"].startswith("gfx950")
+
+
+@pytest.mark.gpu
+def test_shim_conv3_and_tune(tmp_path):
+    case = make_conv3_case(T=3, H=4, W=6, C=32, N=128, pn=True)
+    got, res = run_shim(case, tmp_path, tune={"acc": "f32"})
+    assert_close(got, case.run_oracle(), what="node shim conv3")
+    assert res["plan"]["kernel"] == "mfma"
+
+
+@pytest.mark.gpu
+def test_shim_load_weights(tmp_path):
+    """loadWeights on a converted-model folder (manifest format p0pc0rn-kernels.weights/1, src/convert/encode.js:134)."""
+    rng = np.random.default_rng(5)
+    N, K, M = 128, 256, 4
+    Wq = (rng.standard_normal(N * K) * 0.05).astype(np.float32)
+    q4 = oracle.pack_q4(Wq, N, K)
+    vec = rng.standard_normal(96).astype(np.float32)
+    shard0 = np.concatenate([np.zeros(64, np.uint8), q4])                   # tensor at a non-zero offset
+    shard1 = np.concatenate([np.zeros(16, np.uint8), vec.view(np.uint8)])
+    mdir = tmp_path / "model"
+    mdir.mkdir()
+    shard0.tofile(str(mdir / "w0.bin"))
+    shard1.tofile(str(mdir / "w1.bin"))
+    manifest = {"format": "p0pc0rn-kernels.weights/1",
+                "shards": [{"file": "w0.bin", "bytes": int(shard0.size)}, {"file": "w1.bin", "bytes": int(shard1.size)}],
+                "tensors": {"blk.fc.weight": {"enc": "q4g32a.t64", "file": "w0.bin", "offset": 64, "bytes": int(q4.size),
+                                              "rows": N, "cols": K, "shape": [N, K], "layout": "rows"},
+                            "blk.norm.weight": {"enc": "f32", "file": "w1.bin", "offset": 16, "bytes": 384, "rows": 1,
+                                                "cols": 96, "shape": [96]}}}
+    (mdir / "manifest.json").write_text(json.dumps(manifest))
+    x = oracle.f16_bits(rng.standard_normal(M * K).astype(np.float32))
+    x.tofile(str(tmp_path / "x.bin"))
+    (tmp_path / "spec.json").write_text(json.dumps({"M": M, "N": N, "K": K, "tensor": "blk.fc.weight",
+                                                    "vector": "blk.norm.weight", "vlen": 96}))
+    node("weights", tmp_path)
+    res = json.loads((tmp_path / "result.json").read_text())
+    assert res["progress"] == shard0.size + shard1.size
+    assert sorted(res["names"]) == ["blk.fc.weight", "blk.norm.weight"]
+    assert "not f32" in res["bad"]["message"]
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "v_gpu.f32"), np.float32), vec)
+    y = np.fromfile(str(tmp_path / "y_gpu.bin"), np.uint16)[:M * N]
+    case = make_case(enc="q4g32a.t64", M=M, N=N, K=K, seed=1)
+    case.bufs["w"], case.bufs["x"] = q4, x
+    want = case.run_oracle()
+    assert_close(y, want, fp16=True, what="loadWeights tensor gemm")
