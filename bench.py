@@ -40,6 +40,13 @@ HBM_PEAK = 8.0e12          # B/s, MI355X published
 FP16_PEAK = 2.5e15         # FLOP/s dense fp16 MFMA, MI355X published
 MALL = 256 << 20
 
+# HBM bytes per launch from rocprofv3 counters (profiles/k_gemv_q4_swiglu_decode_M1.md): FETCH_SIZE and WRITE_SIZE in
+# KiB per dispatch, each times what the same counter reads per byte of a plain 1 GiB device copy (`--copy-calib`:
+# FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run, so the
+# figures of the last profiled build are kept here, per workload.
+FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36588, 28)}
+
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -233,8 +240,10 @@ def roofline(wl, ms):
     sec = ms * 1e-3
     if wl.bound == "hbm":
         ach = wl.algo_bytes / sec / 1e9
+        t = TRAFFIC_KIB.get(wl.name)
+        traffic = int((FETCH_FACTOR * t[0] + WRITE_FACTOR * t[1]) * 1024) if t else None
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": None}
+                "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": traffic}
     ach = wl.flops / sec / 1e12
     return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP16_PEAK / 1e12, "unit": "TFLOP/s",
             "frac": round(ach * 1e12 / FP16_PEAK, 4), "traffic": None}
