@@ -240,7 +240,18 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   }
   if (out) *out = p;
   if (plan) {
-    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = kernel == K_MFMA ? 128 : 16; plan->bn = 128;
+    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128;
+    if (kernel == K_MFMA) {
+      mfma_tile(M, N, MI355X_CUS, &plan->bm, &plan->bn);
+      // tuning / test override of the tile (P0K_MFMA_TILE=256x128); results do not depend on it
+      if (const char *ov = getenv("P0K_MFMA_TILE")) {
+        unsigned tm = 0, tn = 0;
+        if (sscanf(ov, "%ux%u", &tm, &tn) == 2 && (tm == 128 || tm == 256) && (tn == 128 || tn == 256)) {
+          plan->bm = tm;
+          plan->bn = tn;
+        }
+      }
+    }
     plan->S = S; plan->KS = KS;
   }
   return P0K_OK;

@@ -147,11 +147,12 @@ __device__ __forceinline__ RowCtx row_ctx(const Params &p, uint32_t row) {
 
 // X' for k = k .. k+7 of row `row` (row < M), as 4 packed fp16 pairs in NATURAL order. (gemm.js:60-95)
 // For conv / conv3, the 8 k lie inside one tap because Ci % 32 == 0 (checked on the host).
-template <int XM>
+// XA: f16 rows are 16-byte aligned (1), not (0), or as F_XALIGN8 says (2; a branch per load).
+template <int XM, int XA = 2>
 __device__ __forceinline__ u32x4 xload8(const Params &p, uint32_t row, const RowCtx &rc, uint32_t k) {
   if constexpr (XM == X_F16) {
     const uint8_t *src = p.X + ((size_t)row * p.ldx + p.kx0 + k) * 2;
-    if (p.flags & F_XALIGN8) return *(const u32x4 *)src;
+    if (XA == 1 || (XA == 2 && (p.flags & F_XALIGN8))) return *(const u32x4 *)src;
     u32x2 lo = *(const u32x2 *)src, hi = *(const u32x2 *)(src + 8);
     return (u32x4){lo.x, lo.y, hi.x, hi.y};
   } else if constexpr (XM == X_RMS || XM == X_LNMOD) {

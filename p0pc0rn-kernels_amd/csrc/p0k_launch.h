@@ -1,13 +1,15 @@
 // p0k_launch.h — host-side launchers of the gfx950 kernels (one per kernel family), called by p0k_runtime.cpp.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace p0k {
 struct Params;
 constexpr int GEMV_MAX_M = 16;
 constexpr unsigned MI355X_CUS = 256;
-// MFMA GEMM (any M): 128 x 128 tiles, 256 threads
-hipError_t launch_gemm_mfma(const Params &p, int we, int xm, hipStream_t s);
+// MFMA GEMM (any M): bm x bn tiles in {128, 256}^2, 512 threads; mfma_tile picks the tile for a shape
+void mfma_tile(uint32_t M, uint32_t N, unsigned cus, unsigned *bm, unsigned *bn);
+hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsigned bn, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
 // (part: S*M*N floats, cnt: one zeroed counter per 128-column tile)
 void gemv_split(const Params &p, int we, unsigned cus, unsigned *S, unsigned *KS);

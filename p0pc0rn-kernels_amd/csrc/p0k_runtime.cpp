@@ -339,7 +339,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream);
   } else {
-    e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, c->stream);
+    e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, plan.bm, plan.bn, c->stream);
   }
   if (e != hipSuccess) return hip_err(e, "gemm launch");
   return P0K_OK;

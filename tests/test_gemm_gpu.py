@@ -243,3 +243,43 @@ def test_gemm_refuses_foreign_and_oversized_buffers(dev):
     finally:
         for b in d.values():
             dev.free(b)
+
+
+# ------------------------------------------------------------------------------------------------ CDNA4 tile shapes
+MFMA_TILES = ["128x128", "256x128", "128x256", "256x256"]
+TILE_CASES = [
+    dict(enc="q4g32a.t64", epi="swiglu", M=300, N=768, K=256, bias=True),
+    dict(enc="q8g64s.t64", xmode="rms", epi="resadd", M=270, N=640, K=256, gate=True),
+    dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=260, N=512, K=128, Hq=2, Hkv=1, Ltot=300, row_off=7),
+    dict(enc="f16", xmode="lnmod", epi="bias", M=140, N=384, K=192, res=True),
+    dict(enc="q4g32a.t64", epi="onormgate", M=129, N=256, K=64),
+]
+
+
+@pytest.mark.parametrize("kw", TILE_CASES, ids=lambda k: f"{k['enc']}-{k.get('xmode', 'f16')}-{k['epi']}")
+def test_every_mfma_tile_matches_oracle(dev, kw, monkeypatch):
+    """Each workgroup tile the library can choose (P0K_MFMA_TILE forces one) gives the oracle's result, and all of them
+    give the same bits (the K order of an output element does not depend on the tile)."""
+    c = make_case(seed=21, **kw)
+    want = c.run_oracle()
+    outs = []
+    for t in MFMA_TILES:
+        banner(f"tile {t} {kw}")
+        monkeypatch.setenv("P0K_MFMA_TILE", t)
+        a = c.args(lambda n: c.bufs[n])
+        assert p0k.select_tile(a)["BM"] == int(t.split("x")[0]) and p0k.select_tile(a)["kernel"] == "mfma"
+        got = c.run_device(dev)
+        assert_close(got, want, fp16=want.dtype == np.uint16, what=f"tile {t}")
+        outs.append(got)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("t", MFMA_TILES)
+def test_conv3_every_mfma_tile_bit_identical(dev, t, monkeypatch):
+    c = make_conv3_case(T=3, H=10, W=12, C=32, N=256, pn=True)
+    base = c.run_device(dev)
+    monkeypatch.setenv("P0K_MFMA_TILE", t)
+    got = c.run_device(dev)
+    assert np.array_equal(got, base)
+    assert_close(got, c.run_oracle(), what=f"conv3 tile {t}")
