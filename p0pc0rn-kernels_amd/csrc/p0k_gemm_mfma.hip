@@ -37,6 +37,7 @@ struct Tile {
   static constexpr int ACH = TBM * 4 / NT;                         // X chunks (8 k) per thread per step
   static constexpr int BCH = TBN * 4 / NT;                         // f16 weight chunks per thread per step
   static constexpr bool PF2 = TBM * TBN < 256 * 256;               // registers for loads two steps ahead
+  static constexpr bool FRAG2 = TBM * TBN < 256 * 256;             // both sub-steps' MFMA operands read at once
 };
 
 // halfs offset of chunk c (8 k) of LDS row r
@@ -71,7 +72,8 @@ struct BRegs<W_F16, TBN> { u32x4 v[TBN * 4 / NT]; };
 
 // AL: the f16 operands (X rows for the f16 prologue, f16 weight rows) allow 16-byte loads
 template <int WE, int XM, int TBM, int TBN, bool AL>
-__global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_mfma(Params p) {
+__global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2))
+__attribute__((amdgpu_waves_per_eu((TBM * TBN >= 256 * 256 ? 1 : 2), (TBM * TBN >= 256 * 256 ? 1 : 2)))) void k_gemm_mfma(Params p) {
   using T = Tile<TBM, TBN>;
   constexpr int UW = WE == W_Q4 ? TBN * 4 / NT : (WE == W_Q8 ? TBN * 8 / NT : 0);
   constexpr int TPR = WE == W_Q4 ? 4 / UW : (WE == W_Q8 ? 8 / UW : 4);   // threads per weight row
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_m
     u32x4 ar[T::ACH];
     BRegs<WE, TBN> br;
   };
-  auto load = [&](Regs &R, uint32_t k0) {
+  auto load = [&](Regs &R, uint32_t k0) __attribute__((always_inline)) {
     u32x4 *ar = R.ar;
     BRegs<WE, TBN> &br = R.br;
 #pragma unroll
@@ -148,7 +150,7 @@ __global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_m
       }
     }
   };
-  auto store = [&](const Regs &R, int stage) {
+  auto store = [&](const Regs &R, int stage) __attribute__((always_inline)) {
     const u32x4 *ar = R.ar;
     const BRegs<WE, TBN> &br = R.br;
     f16 *sA = s0 + stage * T::STAGE, *sB = sA + TBM * BK;
@@ -191,24 +193,40 @@ __global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_m
   const uint32_t nk = p.K / BK;
   // one step of MFMAs on LDS stage `cur`: both 16-k sub-steps' operands are read first, so the second sub-step's
   // reads overlap the first sub-step's MFMAs
-  auto mfma_step = [&](int cur) {
+  auto mfma_step = [&](int cur) __attribute__((always_inline)) {
     const f16 *st = s0 + cur * T::STAGE;
-    f16x8 a[2][T::BI], b[2][T::BJ];
+    if constexpr (T::FRAG2) {
+      f16x8 a[2][T::BI], b[2][T::BJ];
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++) {
-      const int co = (((2 * sub + (lane >> 5)) ^ swz) & 3) * 8;
+      for (int sub = 0; sub < 2; sub++) {
+        const int co = (((2 * sub + (lane >> 5)) ^ swz) & 3) * 8;
 #pragma unroll
-      for (int i = 0; i < T::BI; i++) a[sub][i] = *(const f16x8 *)(st + rdA + i * 32 * BK + co);
+        for (int i = 0; i < T::BI; i++) a[sub][i] = *(const f16x8 *)(st + rdA + i * 32 * BK + co);
 #pragma unroll
-      for (int j = 0; j < T::BJ; j++) b[sub][j] = *(const f16x8 *)(st + rdB + j * 32 * BK + co);
+        for (int j = 0; j < T::BJ; j++) b[sub][j] = *(const f16x8 *)(st + rdB + j * 32 * BK + co);
+      }
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++)
+#pragma unroll
+        for (int i = 0; i < T::BI; i++)
+#pragma unroll
+          for (int j = 0; j < T::BJ; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i], b[sub][j], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < 2; sub++) {
+        const int co = (((2 * sub + (lane >> 5)) ^ swz) & 3) * 8;
+        f16x8 a[T::BI], b[T::BJ];
+#pragma unroll
+        for (int i = 0; i < T::BI; i++) a[i] = *(const f16x8 *)(st + rdA + i * 32 * BK + co);
+#pragma unroll
+        for (int j = 0; j < T::BJ; j++) b[j] = *(const f16x8 *)(st + rdB + j * 32 * BK + co);
+#pragma unroll
+        for (int i = 0; i < T::BI; i++)
+#pragma unroll
+          for (int j = 0; j < T::BJ; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      }
     }
-#pragma unroll
-    for (int sub = 0; sub < 2; sub++)
-#pragma unroll
-      for (int i = 0; i < T::BI; i++)
-#pragma unroll
-        for (int j = 0; j < T::BJ; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i], b[sub][j], acc[i][j], 0, 0, 0);
   };
   // Loads and LDS writes are unconditional (past the last step they reload the last step and write the idle stage),
   // so the compiler can count outstanding loads exactly and wait only for the step it writes.
@@ -217,9 +235,11 @@ __global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_m
   if constexpr (T::PF2) {
     // loads run two steps ahead of the MFMAs: registers R0 / R1 alternate, LDS stages alternate
     Regs R0, R1;
-    auto step = [&](uint32_t kt, Regs &Rnext2, const Regs &Rnext) {
+    auto step = [&](uint32_t kt, Regs &Rnext2, const Regs &Rnext) __attribute__((always_inline)) {
       load(Rnext2, kclamp((kt + 2) * BK));
+      __builtin_amdgcn_sched_barrier(0);   // keep the loads at the top of the step (issued before the MFMAs)
       mfma_step(kt & 1);
+      __builtin_amdgcn_sched_barrier(0);
       store(Rnext, (kt & 1) ^ 1);
       __syncthreads();
     };
@@ -243,7 +263,9 @@ __global__ __launch_bounds__(NT, (TBM * TBN >= 256 * 256 ? 1 : 2)) void k_gemm_m
     __syncthreads();
     for (uint32_t kt = 0; kt < nk; kt++) {
       load(R, kclamp((kt + 1) * BK));
+      __builtin_amdgcn_sched_barrier(0);
       mfma_step(kt & 1);
+      __builtin_amdgcn_sched_barrier(0);
       store(R, (kt & 1) ^ 1);
       __syncthreads();
     }
@@ -314,12 +336,14 @@ static hipError_t launch_x(const Params &p, int xm, unsigned bm, unsigned bn, hi
 }
 
 // The tile: the largest that still gives the CUs work. Larger tiles do less dequant / prologue work and read less
-// LDS per MFMA; when the grid would leave CUs idle (or a large part of the last round of workgroups empty), smaller
+// LDS per MFMA (128 x 256 with two workgroups per CU measures best; 256 x 256 runs one wave per SIMD and hides less
+// latency); when the grid would leave CUs idle (or a large part of the last round of workgroups empty), smaller
 // tiles win. Each candidate is scored by its relative per-CU rate times the fraction of workgroup slots (one per CU
 // for 256 x 256, two for the others) that hold real work over the rounds the grid needs.
 void mfma_tile(uint32_t M, uint32_t N, unsigned cus, unsigned *bm, unsigned *bn) {
+  // relative rates measured on MI355X (4096^3, f16 / q4 / q8 weights, f16 / rms / lnmod prologues)
   struct C { unsigned m, n, per_cu; double rate; } cand[] = {
-      {256, 256, 1, 1.0}, {256, 128, 2, 0.85}, {128, 256, 2, 0.85}, {128, 128, 2, 0.6}};
+      {128, 256, 2, 1.0}, {256, 128, 2, 0.92}, {256, 256, 1, 0.9}, {128, 128, 2, 0.75}};
   double best = -1.0;
   for (const C &c : cand) {
     if (c.n == 256 && N <= 128) continue;

@@ -135,8 +135,9 @@ def test_kernel_choice():
     assert p0k.lib().p0k_gemm_flops(C.byref(p0k.gemm_args(host_args(make_case(M=3, N=64, K=32)), p0k.numpy_resolve))) == 2 * 3 * 64 * 32
 
 
-@pytest.mark.parametrize("M,N,tile", [(4096, 24576, (256, 256)), (2048, 4096, (128, 128)), (4096, 9216, (256, 256)),
-                                      (191360, 128, (256, 128)), (20000, 128, (128, 128)), (100, 128, (128, 128)), (64, 2048, (128, 128))])
+@pytest.mark.parametrize("M,N,tile", [(4096, 24576, (128, 256)), (2048, 4096, (128, 128)), (4096, 9216, (128, 256)),
+                                      (191360, 128, (128, 128)), (20000, 128, (128, 128)), (100, 128, (128, 128)),
+                                      (64, 2048, (128, 128)), (8192, 8192, (128, 256))])
 def test_mfma_tile_choice(M, N, tile):
     """Large tiles when the grid still fills the 256 CUs; smaller ones when it would leave them idle."""
     t = p0k.select_tile(host_args(make_case(M=M, N=N, K=32)))
