@@ -223,47 +223,25 @@ __device__ __forceinline__ void store_f16x8(uint8_t *yb, size_t idx, const float
   }
 }
 
+// sum over the 16 lanes of an aligned lane group (the 16 threads that share one row in the epilogue)
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 16);
+  return v;
+}
+
 // Apply the epilogue to rows [0, R) x 128 ws columns of an fp32 tile C (row stride ldc) whose first row is output row
-// mB and first ws column is nB. Every thread of the block calls it (NT threads).
+// mB and first ws column is nB. Every thread of the block calls it (NT threads, NT % 16 == 0). Sixteen consecutive
+// threads share one row, each owning 8 consecutive columns, so stores are 16 bytes and row reductions are shuffles.
 template <int NT>
 __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32_t mB, uint32_t nB, int tid) {
   const int epi = p.epi;
-  if (epi == E_F16 || epi == E_F32 || epi == E_BIAS || epi == E_RESADD) {            // gemm.js:194-203, 211-215
-    for (int t = tid; t < R * 16; t += NT) {
-      int r = t >> 4, ch = t & 15;
-      uint32_t m = mB + r, col = nB + ch * 8;
-      if (m >= p.M || col >= p.N) continue;
-      uint32_t nv = p.N - col;
-      float v[8];
-      const f32x4 *src = (const f32x4 *)(C + r * ldc + ch * 8);
-      f32x4 a0 = src[0], a1 = src[1];
-      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-      size_t yi = (size_t)m * p.ldy + p.ny0 + col;
-      if (epi == E_F16) {
-        store_f16x8(p.Y, yi, v, nv);
-      } else if (epi == E_F32) {
-        float *y = (float *)p.Y + yi;
-        for (uint32_t j = 0; j < 8 && j < nv; j++) y[j] = v[j];
-      } else if (epi == E_BIAS) {                                                   // f16(acc + b[n] (+ Y))
-        const float *b = p.EV + p.evOff + col;
-        const uint16_t *yh = (const uint16_t *)p.Y + yi;
-        for (uint32_t j = 0; j < 8 && j < nv; j++) {
-          v[j] += b[j];
-          if (p.flags & F_RES) v[j] += h_val(yh[j]);
-        }
-        store_f16x8(p.Y, yi, v, nv);
-      } else {                                                                      // R += gate[n] * (acc + bias[n])
-        float *y = (float *)p.Y + yi;
-        for (uint32_t j = 0; j < 8 && j < nv; j++) {
-          float g = (p.flags & F_GATE) ? p.EV[p.evOff + col + j] : 1.0f;
-          float b = (p.flags & F_BIAS) ? p.BV[p.bvOff + col + j] : 0.0f;
-          float prev = (p.flags & F_STORE) ? 0.0f : y[j];
-          y[j] = prev + g * (v[j] + b);
-        }
-      }
-    }
-  } else if (epi == E_SWIGLU) {                                                     // gemm.js:204-210
+  const int g = tid & 15;                       // 8-column group of the row
+  constexpr int RPP = NT / 16;                  // rows per pass
+  if (epi == E_SWIGLU) {                                                           // gemm.js:204-210
+    // 8 output columns (16 ws columns, interleaved gate / up) per thread, 8 threads per row
     const uint32_t Nout = p.N >> 1;
+    const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
     for (int t = tid; t < R * 8; t += NT) {
       int r = t >> 3, ch = t & 7;
       uint32_t m = mB + r, o = (nB >> 1) + ch * 8;
@@ -272,77 +250,128 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        float g = src[2 * j], u = src[2 * j + 1];
-        if ((p.flags & F_BIAS) && o + j < Nout) { g += p.BV[p.bvOff + o + j]; u += p.BV[p.bvOff + p.bvUp + o + j]; }
+        float gt = src[2 * j], u = src[2 * j + 1];
+        if (bias && o + j < Nout) { gt += p.BV[p.bvOff + o + j]; u += p.BV[p.bvOff + p.bvUp + o + j]; }
         float act;
-        if (p.flags & F_GELU) {
-          float z = 0.7978845608f * (g + 0.044715f * g * g * g);
+        if (gelu) {
+          float z = 0.7978845608f * (gt + 0.044715f * gt * gt * gt);
           z = fminf(fmaxf(z, -15.0f), 15.0f);
-          act = g * 0.5f * (1.0f + tanhf(z));
+          act = gt * 0.5f * (1.0f + tanhf(z));
         } else {
-          act = g / (1.0f + __expf(-g));
+          act = gt / (1.0f + __expf(-gt));
         }
         v[j] = act * u;
       }
       store_f16x8(p.Y, (size_t)m * p.ldy + p.ny0 + o, v, Nout - o);
     }
-  } else if (epi == E_HEADS) {                                                      // gemm.js:216-253
-    const uint32_t hd = nB >> 7;
-    const int sec = hd < p.Hq ? 0 : (hd < p.Hq + p.Hkv ? 1 : 2);
-    const float *nw = p.EV + p.evOff + (sec ? 128 : 0);
-    const bool half = p.flags & F_ROPE_HALF;
-    for (int r = tid; r < R; r += NT) {
-      uint32_t m = mB + r;
-      if (m >= p.M) continue;
-      const float *src = C + r * ldc;
-      uint32_t row = p.rowOff + m;
-      uint16_t *y = (uint16_t *)p.Y + ((size_t)hd * p.Ltot + row) * 128;
-      float inv = 1.0f;
+    return;
+  }
+  for (int r0 = 0; r0 < R; r0 += RPP) {
+    const int r = r0 + (tid >> 4);
+    const uint32_t m = mB + r;
+    const bool live = r < R && m < p.M;            // whole 16-lane groups agree, so the shuffles below are safe
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < R) {
+      const f32x4 *src = (const f32x4 *)(C + r * ldc + g * 8);
+      f32x4 a0 = src[0], a1 = src[1];
+      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    }
+    if (epi == E_HEADS) {                                                          // gemm.js:216-253
+      const uint32_t hd = nB >> 7;
+      const int sec = hd < p.Hq ? 0 : (hd < p.Hq + p.Hkv ? 1 : 2);
+      const int d0 = g * 8;
       if (sec < 2) {
         float ss = 0.0f;
-        for (int d = 0; d < 128; d++) ss += src[d] * src[d];
-        inv = __frsqrt_rn(ss / 128.0f + p.eps);
-      }
-      const float *rp = p.RP + (size_t)row * 128;
-      for (int d0 = 0; d0 < 128; d0 += 8) {
-        float v[8];
-        if (sec == 2) {
-          for (int j = 0; j < 8; j++) v[j] = src[d0 + j];
-        } else if (!half) {                      // interleaved pairs (2p, 2p+1), angle p
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss += v[j] * v[j];
+        ss = sum16(ss);
+        const float inv = __frsqrt_rn(ss / 128.0f + p.eps);
+        const float *nw = p.EV + p.evOff + (sec ? 128 : 0);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = v[j] * inv * nw[d0 + j];
+        const uint32_t row = p.rowOff + (live ? m : 0u);
+        const float *rp = p.RP + (size_t)row * 128;
+        if (!(p.flags & F_ROPE_HALF)) {          // interleaved pairs (2p, 2p+1), angle p
+#pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            int d = d0 + j;
-            float x0 = src[d] * inv * nw[d], x1 = src[d + 1] * inv * nw[d + 1];
-            float cs = rp[d], sn = rp[d + 1];
-            v[j] = x0 * cs - x1 * sn; v[j + 1] = x0 * sn + x1 * cs;
+            const float cs = rp[d0 + j], sn = rp[d0 + j + 1];
+            v[j] = x[j] * cs - x[j + 1] * sn;
+            v[j + 1] = x[j] * sn + x[j + 1] * cs;
           }
-        } else {                                 // rotate-half pairs (d, d+64), angle d
+        } else {                                 // rotate-half pairs (d, d+64): the partner columns are 8 groups away
+          float y[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) y[j] = __shfl_xor(x[j], 8, 16);
+          const bool lo = d0 < 64;
+#pragma unroll
           for (int j = 0; j < 8; j++) {
-            int d = d0 + j, dl = d & 63;
-            float lo = src[dl] * inv * nw[dl], hi = src[dl + 64] * inv * nw[dl + 64];
-            float cs = rp[2 * dl], sn = rp[2 * dl + 1];
-            v[j] = d < 64 ? lo * cs - hi * sn : hi * cs + lo * sn;
+            const int dl = (d0 + j) & 63;
+            const float cs = rp[2 * dl], sn = rp[2 * dl + 1];
+            v[j] = lo ? x[j] * cs - y[j] * sn : x[j] * cs + y[j] * sn;
           }
         }
-        store_f16x8((uint8_t *)y, d0, v, 8);
       }
+      if (live) store_f16x8(p.Y, ((size_t)hd * p.Ltot + p.rowOff + m) * 128 + d0, v, 8);
+      continue;
     }
-  } else if (epi == E_ONORMGATE) {                                                  // gemm.js:227-232
-    for (int r = tid; r < R; r += NT) {
-      uint32_t m = mB + r;
-      if (m >= p.M) continue;
-      const float *src = C + r * ldc;
+    if (epi == E_ONORMGATE) {                                                      // gemm.js:227-232
       float ss = 0.0f;
-      for (int d = 0; d < 128; d++) ss += src[d] * src[d];
-      float inv = __frsqrt_rn(ss / 128.0f + p.eps);
-      const uint16_t *gt = p.GT + (size_t)m * p.Ltot + p.ny0 + nB;
-      size_t yi = (size_t)m * p.ldy + p.ny0 + nB;
-      for (int d0 = 0; d0 < 128; d0 += 8) {
-        float v[8];
-        for (int j = 0; j < 8; j++) {
-          int d = d0 + j;
-          v[j] = src[d] * inv * p.EV[p.evOff + d] / (1.0f + __expf(-h_val(gt[d])));
-        }
-        if (nB + d0 < p.N) store_f16x8(p.Y, yi + d0, v, p.N - (nB + d0));
+#pragma unroll
+      for (int j = 0; j < 8; j++) ss += v[j] * v[j];
+      ss = sum16(ss);
+      const float inv = __frsqrt_rn(ss / 128.0f + p.eps);
+      const uint32_t col = nB + g * 8;
+      if (live && col < p.N) {
+        const uint16_t *gt = p.GT + (size_t)m * p.Ltot + p.ny0 + col;
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = v[j] * inv * p.EV[p.evOff + g * 8 + j] / (1.0f + __expf(-h_val(gt[j])));
+        store_f16x8(p.Y, (size_t)m * p.ldy + p.ny0 + col, v, p.N - col);
+      }
+      continue;
+    }
+    // f16 / f32 / bias / resadd (gemm.js:194-203, 211-215)
+    const uint32_t col = nB + g * 8;
+    if (!live || col >= p.N) continue;
+    const uint32_t nv = p.N - col;
+    const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
+    if (epi == E_F16) {
+      store_f16x8(p.Y, yi, v, nv);
+    } else if (epi == E_F32) {
+      float *y = (float *)p.Y + yi;
+      if (nv >= 8 && (((uintptr_t)y) & 15u) == 0) {
+        ((f32x4 *)y)[0] = (f32x4){v[0], v[1], v[2], v[3]};
+        ((f32x4 *)y)[1] = (f32x4){v[4], v[5], v[6], v[7]};
+      } else {
+        for (uint32_t j = 0; j < 8 && j < nv; j++) y[j] = v[j];
+      }
+    } else if (epi == E_BIAS) {                                                   // f16(acc + b[n] (+ Y))
+      const float *b = p.EV + p.evOff + col;
+      const uint16_t *yh = (const uint16_t *)p.Y + yi;
+      const bool res = p.flags & F_RES;
+      for (uint32_t j = 0; j < 8 && j < nv; j++) {
+        float t = v[j] + b[j];
+        if (res) t += h_val(yh[j]);
+        v[j] = t;
+      }
+      store_f16x8(p.Y, yi, v, nv);
+    } else {                                                                       // R += gate[n] * (acc + bias[n])
+      float *y = (float *)p.Y + yi;
+      const bool gate = p.flags & F_GATE, bias = p.flags & F_BIAS, st = p.flags & F_STORE;
+      float gv[8], bv[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        gv[j] = (gate && (uint32_t)j < nv) ? p.EV[p.evOff + col + j] : 1.0f;
+        bv[j] = (bias && (uint32_t)j < nv) ? p.BV[p.bvOff + col + j] : 0.0f;
+      }
+      if (nv >= 8 && (((uintptr_t)y) & 15u) == 0) {
+        f32x4 p0 = st ? (f32x4){0, 0, 0, 0} : ((const f32x4 *)y)[0], p1 = st ? (f32x4){0, 0, 0, 0} : ((const f32x4 *)y)[1];
+        ((f32x4 *)y)[0] = (f32x4){p0.x + gv[0] * (v[0] + bv[0]), p0.y + gv[1] * (v[1] + bv[1]), p0.z + gv[2] * (v[2] + bv[2]),
+                                  p0.w + gv[3] * (v[3] + bv[3])};
+        ((f32x4 *)y)[1] = (f32x4){p1.x + gv[4] * (v[4] + bv[4]), p1.y + gv[5] * (v[5] + bv[5]), p1.z + gv[6] * (v[6] + bv[6]),
+                                  p1.w + gv[7] * (v[7] + bv[7])};
+      } else {
+        for (uint32_t j = 0; j < 8 && j < nv; j++) y[j] = (st ? 0.0f : y[j]) + gv[j] * (v[j] + bv[j]);
       }
     }
   }
