@@ -111,7 +111,7 @@ typedef struct p0k_rowstats_args {
   float *st_buf; uint32_t st_off; uint64_t st_size;
 } p0k_rowstats_args;
 
-typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM, 1 = GEMV (M <= 16) */
+typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM, 1 = GEMV (M = 1), 2 = MFMA GEMV (2 <= M <= 16) */
   p0k_tile;
 
 typedef struct p0k_pool_stats {

@@ -229,13 +229,15 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
     // and addresses the tensor with 32-bit offsets
     if ((we != P0K_ENC_Q8G64S_T64 || a->wk0 % 64 == 0) && (we != P0K_ENC_F16 || (f & F_WALIGN8)) &&
         wbytes < (1ull << 32)) {
-      gemv_split(p, we, MI355X_CUS, &S, &KS);
+      // one row: the VALU stream (exact dot products of fp32-dequantised weights); 2..16 rows: the matrix cores
+      const bool mf = M >= 2;
+      gemv_split(p, we, MI355X_CUS, mf, &S, &KS);
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
       if (const char *ov = getenv("P0K_GEMV_SLICES")) {
         unsigned s2 = (unsigned)atoi(ov), quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
-        if (s2 && K % (s2 * quant) == 0) { S = s2; KS = K / s2; }
+        if (s2 && K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, mf)) { S = s2; KS = K / s2; }
       }
-      if (S) kernel = K_GEMV;
+      if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
     }
   }
   if (out) *out = p;

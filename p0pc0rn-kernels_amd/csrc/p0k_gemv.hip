@@ -46,6 +46,53 @@ struct Unit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
 template <int MT>
 constexpr int ks_max() { return (GV_LDS * 8 / (MT * 18)) & ~1023; }
 
+// After the stream: the K-quarter partials of the item are in sR as [quarter][m][128 ws columns]; sum them, meet the
+// other slices of the tile when S > 1, and run the epilogue.
+template <int MT>
+__device__ __forceinline__ void finish(const Params &p, float *sR, float *part, uint32_t *cnt, uint32_t S, uint32_t tile,
+                                       uint32_t slice, uint32_t nB, int tid, uint32_t *sLast_) {
+  uint32_t &sLast = *sLast_;
+  for (int t = tid; t < MT * 128; t += GV_NT) {
+    float s = sR[t];
+#pragma unroll
+    for (int q = 1; q < GV_KSUB; q++) s += sR[q * MT * 128 + t];
+    sR[t] = s;
+  }
+  __syncthreads();
+
+  if (S > 1) {
+    // partial tile -> workspace [slice][m][ws column, padded to whole tiles]. The partials, the counter and the reads
+    // of the last item all go to the memory side (system-coherent accesses that skip the per-XCD L2s), so items on
+    // different XCDs meet without any L2 writeback or invalidation: a store is acknowledged only once it is there,
+    // and every thread waits for its acknowledgements before the barrier that precedes the counter update.
+    const uint32_t Np = gridDim.x / S * 128u;
+    const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+      uint32_t m = t >> 7, c = t & 127;
+      __hip_atomic_store(part + ((size_t)slice * p.M + m) * Np + nB + c, sR[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t old = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sLast = (old == S - 1u) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+      uint32_t m = t >> 7, c = t & 127;
+      const float *src = part + (size_t)m * Np + nB + c;
+      float s = 0.0f;
+      for (uint32_t q = 0; q < S; q++)
+        s += __hip_atomic_load(src + (size_t)q * p.M * Np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sR[t] = s;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+  }
+  epilogue<GV_NT>(p, sR, 128, MT, 0u, nB, tid);
+}
+
 template <int WE, int XM, int MT>
 __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
   constexpr int UK = Unit<WE>::UK, PF = Unit<WE>::PF, KSM = ks_max<MT>(), NGM = KSM / UK;
@@ -227,57 +274,249 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 #pragma unroll
   for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + ch * 64 + lane] = acc[m];
   __syncthreads();
-  for (int t = tid; t < MT * 128; t += GV_NT) {
-    float s = sR[t];
+  finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Decode on the matrix cores (2 <= M <= 16). With several rows of X the per-row dot products of the stream above
+// multiply its VALU work; here the same items, waves and ring feed v_mfma_f32_16x16x32_f16 instead. Per 32-k step
+// (q4, f16; 64-k for q8) a wave runs one MFMA per block of 16 of its 64 weight rows: A = X' (16 rows, zero past M),
+// B = the block's weights. Lane l supplies, for block i, weight row 16 i + l%16 and the 8 k at 8 (l/16) of the step
+// (one q4 code word, two q8 words or 16 f16 bytes, each load instruction covering 16 whole rows), and receives
+// D[m = 4 (l/16) + r][row 16 i + l%16], r = 0..3: every lane keeps ONE weight row per block, so the row's scale and
+// minimum apply in registers. The weights are never dequantised: the MFMA multiplies the magic-biased codes, as in
+// the stream above, and the per-group corrections come from X' sums staged with X':
+//   q4: B holds 1024 + q (low nibbles) and 1024 + 16 q (high nibbles, in place), A holds x and x / 16 at those
+//       positions, so D = sum x q + G1 with G1 = 1024 X_lo + 64 X_hi; y += s (D - G1) + mn (X_lo + X_hi)
+//   q8: B holds 1152 + q; y += s (D - 1152 X)
+//   f16: B holds the weights; D accumulates across steps in the MFMA.
+// This is the fp32 arithmetic of the reference's CPU path (cpuGemm over fp32 dequantised weights) like the stream
+// above, and for x a unit vector it returns the dequantised weight f16(f32(q*s + mn)) / f16(q*s) exactly.
+template <int WE>
+struct MUnit;
+template <>
+struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 8; u32x4 code; uint32_t sm; };   // row `lane`, as loaded
+template <>
+struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x2 code[4][2]; uint32_t s[4]; };
+template <>
+struct MUnit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
+
+constexpr int MF_KSM = 4096;                                // longest K slice of one item
+constexpr int MF_XG = 16 * MF_KSM * 2 + 16 * (MF_KSM / 32) * 8;    // X' of 16 rows + (G1, G2) per row and group
+constexpr int MF_LDS = MF_XG + 8 * 64 * 20;                 // + per wave: one q4 unit (64 rows x 16 B) and its scales
+
+template <int WE, int XM>
+__global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
+  constexpr int MT = 16;
+  constexpr int UK = MUnit<WE>::UK, PF = MUnit<WE>::PF, KSM = MF_KSM;
+  static_assert(GV_KSUB * MT * 128 * 4 <= MF_LDS, "partials must fit the staging buffer");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[MF_LDS];
+  __shared__ uint32_t sLast;
+  f16 *sX = (f16 *)smem;                                       // [MT][KSM] X', pair order of the encoding
+  f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [unit][MT] (G1, G2)
+  float *sR = (float *)smem;                                   // after the stream: partials
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ch = wave / GV_KSUB, sub = wave % GV_KSUB, l16 = lane & 15, kc = lane >> 4;
+  const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
+  const uint32_t nB = tile * 128u, kb0 = slice * KS;
+  const uint32_t nuw = KS / UK / GV_KSUB, u0 = sub * nuw;
+
+  // q4: lane l loads weight row l of the wave's 64 (16 bytes + its scale word, as the one-row stream does) and the
+  // wave regroups the unit through its own LDS slot; q8 / f16: per block, this lane's weight row and the byte offsets
+  // of its codes and scale in the slice's first unit
+  uint32_t *wsw = (uint32_t *)(smem + MF_XG) + wave * 320;     // [64 rows][4 words] then [64] scale words
+  uint32_t woff[4], soff[4], rlo[4];
 #pragma unroll
-    for (int q = 1; q < GV_KSUB; q++) s += sR[q * MT * 128 + t];
-    sR[t] = s;
+  for (int i = 0; i < 4; i++) {
+    const uint32_t r = wrow(p, nB + ch * 64 + (WE == W_Q4 ? lane : 16 * i + l16));
+    rlo[i] = r & 1u;
+    if constexpr (WE == W_Q4) {
+      const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5)) * 1280u;
+      woff[i] = rec + (r & 63u) * 16u;
+      soff[i] = rec + 1024u + (r & 63u) * 4u;
+    } else if constexpr (WE == W_Q8) {
+      const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 6)) * 4224u;
+      woff[i] = rec + (r & 63u) * 64u + kc * 8u;
+      soff[i] = rec + 4096u + (r & 62u) * 2u;
+    } else {
+      woff[i] = (r * p.wG + p.wk0 + kb0) * 2u + kc * 16u;
+      soff[i] = 0u;
+    }
+  }
+  constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
+
+  auto load = [&](MUnit<WE> &u, uint32_t unit) {
+    const uint32_t du = unit * USTRIDE;
+    if constexpr (WE == W_Q4) {
+      u.code = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[0] + du)));
+      u.sm = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[0] + du)));
+    } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if constexpr (WE == W_Q8) {
+        u.code[i][0] = __builtin_nontemporal_load((const u32x2 *)(p.W + (woff[i] + du)));
+        u.code[i][1] = __builtin_nontemporal_load((const u32x2 *)(p.W + (woff[i] + du + 32u)));
+        u.s[i] = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[i] + du)));
+      } else {
+        u.v[i] = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[i] + du)));
+      }
+    }
+    }
+  };
+
+  // the nibble masks, the fp16 exponent and the q8 bias in registers (gfx9 VOP3 takes no literal operands)
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mag = 0x64006400u, m64 = 0x64646464u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi), "+v"(mag), "+v"(m64));
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) acc[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const MUnit<WE> &u, uint32_t unit) {
+    if constexpr (WE == W_F16) {
+      const f16x8 a = *(const f16x8 *)(sX + l16 * KSM + unit * UK + kc * 8);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const f16x8 b = __builtin_bit_cast(f16x8, u.v[i]);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+      }
+    } else {
+      // (G1, G2) of rows m = 4 kc + r for this unit
+      const f32x4 *gp = (const f32x4 *)(sG + unit * MT + 4 * kc);
+      const f32x4 ga = gp[0], gb = gp[1];
+      const float g1[4] = {ga.x, ga.z, gb.x, gb.z}, g2[4] = {ga.y, ga.w, gb.y, gb.w};
+      f32x4 d[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) d[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+      // q4: regroup the unit inside the wave: lane (kc, l16) takes word kc of row 16 i + l16 and that row's scale
+      uint32_t qw[4], qs[4];
+      if constexpr (WE == W_Q4) {
+        *(u32x4 *)(wsw + 4 * lane) = u.code;
+        wsw[256 + lane] = u.sm;
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          qw[i] = wsw[4 * (16 * i + l16) + kc];
+          qs[i] = wsw[256 + 16 * i + l16];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+      }
+#pragma unroll
+      for (int h = 0; h < UK / 32; h++) {
+        const f16x8 a = *(const f16x8 *)(sX + l16 * KSM + unit * UK + h * 32 + kc * 8);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          u32x4 bw;
+          if constexpr (WE == W_Q4) {
+            const uint32_t w = qw[i], w8 = w >> 8;
+            bw = (u32x4){(w & mlo) | mag, (w & mhi) | mag, (w8 & mlo) | mag, (w8 & mhi) | mag};
+          } else {
+            const uint32_t x0 = u.code[i][h].x ^ 0x80808080u, x1 = u.code[i][h].y ^ 0x80808080u;
+            bw = (u32x4){perm(m64, x0, 0x04020400u), perm(m64, x0, 0x04030401u), perm(m64, x1, 0x04020400u),
+                         perm(m64, x1, 0x04030401u)};
+          }
+          d[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bw), d[i], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float s, mn = 0.0f;
+        if constexpr (WE == W_Q4) {
+          const f16x2 sm2 = as_h2(qs[i]);
+          s = (float)sm2.x; mn = (float)sm2.y;
+        } else {
+          s = (float)__builtin_bit_cast(f16, (uint16_t)(rlo[i] ? (u.s[i] >> 16) : (u.s[i] & 0xffffu)));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][r] = fmaf(s, d[i][r] - g1[r], fmaf(mn, g2[r], acc[i][r]));
+      }
+    }
+  };
+
+  MUnit<WE> ring[PF];
+#pragma unroll
+  for (int j = 0; j < PF; j++)
+    if ((uint32_t)j < nuw) load(ring[j], u0 + j);
+
+  // X' of the slice -> LDS (rows past M are zero); q4: the high-nibble positions (odd pair slots) hold x / 16
+  const uint32_t nb = KS / 8, ng = KS / UK;
+  for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
+    uint32_t m = t / nb, kq = t - m * nb;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (m < p.M) v = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq));
+    *(u32x4 *)(sX + m * KSM + 8 * kq) = v;
+  }
+  if constexpr (WE != W_F16) {
+    __syncthreads();
+    // per (row, unit): sums of the unscaled X' over the low / high positions -> (G1, G2); then scale the q4 high slots
+    for (uint32_t t = tid; t < MT * ng; t += GV_NT) {
+      uint32_t g = t / MT, m = t - g * MT;
+      const u32x4 *x4 = (const u32x4 *)(sX + m * KSM + g * UK);
+      float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+      for (int q = 0; q < UK / 8; q++) {
+        const u32x4 xv = x4[q];
+        const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
+        lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
+        hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
+      }
+      if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
+      else sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
+    }
+    __syncthreads();
+    if constexpr (WE == W_Q4) {
+      const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+      for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
+        uint32_t m = t / nb, kq = t - m * nb;
+        u32x4 *px = (u32x4 *)(sX + m * KSM + 8 * kq);
+        u32x4 v = *px;
+        v.y = as_u(as_h2(v.y) * r16);
+        v.w = as_u(as_h2(v.w) * r16);
+        *px = v;
+      }
+    }
   }
   __syncthreads();
 
-  if (S > 1) {
-    // partial tile -> workspace [slice][m][ws column, padded to whole tiles]. The partials, the counter and the reads
-    // of the last item all go to the memory side (system-coherent accesses that skip the per-XCD L2s), so items on
-    // different XCDs meet without any L2 writeback or invalidation: a store is acknowledged only once it is there,
-    // and every thread waits for its acknowledgements before the barrier that precedes the counter update.
-    const uint32_t Np = gridDim.x / S * 128u;
-    const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
-    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
-      uint32_t m = t >> 7, c = t & 127;
-      __hip_atomic_store(part + ((size_t)slice * p.M + m) * Np + nB + c, sR[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  uint32_t j0 = 0;
+#pragma unroll 1
+  for (; j0 + PF <= nuw; j0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      compute(ring[j], u0 + j0 + j);
+      const uint32_t nx = j0 + PF + j;
+      load(ring[j], u0 + (nx < nuw ? nx : nuw - 1u));
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t old = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      sLast = (old == S - 1u) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!sLast) return;
-    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
-      uint32_t m = t >> 7, c = t & 127;
-      const float *src = part + (size_t)m * Np + nB + c;
-      float s = 0.0f;
-      for (uint32_t q = 0; q < S; q++)
-        s += __hip_atomic_load(src + (size_t)q * p.M * Np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      sR[t] = s;
-    }
-    if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __syncthreads();
   }
-  epilogue<GV_NT>(p, sR, 128, MT, 0u, nB, tid);
+#pragma unroll
+  for (int j = 0; j < PF; j++)
+    if (j0 + j < nuw) compute(ring[j], u0 + j0 + j);
+  __syncthreads();                                             // X' is dead: the buffer takes the partials
+
+  // D[m = 4 kc + r][row 16 i + l16]
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + ch * 64 + 16 * i + l16] = acc[i][r];
+  __syncthreads();
+  finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
-static uint32_t ks_max_of(uint32_t M) {
+static uint32_t ks_max_of(uint32_t M, bool mf) {
+  if (mf) return MF_KSM;
   return M <= 1 ? ks_max<1>() : M <= 2 ? ks_max<2>() : M <= 4 ? ks_max<4>() : M <= 8 ? ks_max<8>() : ks_max<16>();
 }
+unsigned gemv_ks_max(unsigned M, bool mf) { return ks_max_of(M, mf); }
 
 // Slices per tile: the fewest that fill the GPU with items (about one per CU) and keep each slice's X' inside the LDS
 // budget, with a whole number of units per K-quarter.
-void gemv_split(const Params &p, int we, unsigned cus, unsigned *S_out, unsigned *KS_out) {
+void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S_out, unsigned *KS_out) {
   const uint32_t tiles = (p.N + 127) / 128;
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;     // k per "one unit in each K-quarter"
-  const uint32_t ksm = ks_max_of(p.M);
+  const uint32_t ksm = ks_max_of(p.M, mf);
   uint32_t S = 1;
   while ((tiles * S < cus * 7u / 8u || p.K / S > ksm) && p.K % (2u * S * quant) == 0) S *= 2u;
   if (p.K % (S * quant) != 0 || p.K / S > ksm) S = 0;             // caller falls back to the MFMA kernel
@@ -293,7 +532,13 @@ static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t 
   return hipGetLastError();
 }
 template <int WE, int XM>
-static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
+static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s, bool mf) {
+  if (mf) {
+    if (KS > (uint32_t)MF_KSM) return hipErrorInvalidValue;
+    dim3 grid(((p.N + 127) / 128) * S);
+    hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+    return hipGetLastError();
+  }
   if (p.M <= 1) return launch3<WE, XM, 1>(p, part, cnt, S, KS, s);
   if (p.M <= 2) return launch3<WE, XM, 2>(p, part, cnt, S, KS, s);
   if (p.M <= 4) return launch3<WE, XM, 4>(p, part, cnt, S, KS, s);
@@ -301,23 +546,24 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
   return launch3<WE, XM, 16>(p, part, cnt, S, KS, s);
 }
 template <int WE>
-static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
+static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s,
+                          bool mf) {
   switch (xm) {
-  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s);
-  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s);
-  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s);
+  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf);
+  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf);
+  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
-                       hipStream_t s) {
+                       hipStream_t s, bool mf) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
   switch (we) {
-  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s);
-  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s);
-  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s);
+  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf);
+  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf);
+  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf);
   }
   return hipErrorInvalidValue;
 }

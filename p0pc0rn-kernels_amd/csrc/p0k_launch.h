@@ -11,9 +11,11 @@ constexpr unsigned MI355X_CUS = 256;
 void mfma_tile(uint32_t M, uint32_t N, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsigned bn, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
-// (part: S*M*N floats, cnt: one zeroed counter per 128-column tile)
-void gemv_split(const Params &p, int we, unsigned cus, unsigned *S, unsigned *KS);
-hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s);
+// (part: S*M*N floats, cnt: one zeroed counter per 128-column tile). mf: the matrix-core variant (2 <= M <= 16).
+void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S, unsigned *KS);
+unsigned gemv_ks_max(unsigned M, bool mf);   // longest K slice one item stages
+hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s,
+                       bool mf);
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);

@@ -316,7 +316,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   p.GT = (const uint16_t *)a->gt_buf;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
   hipError_t e;
-  if (plan.kernel == p0k::K_GEMV) {
+  if (plan.kernel == p0k::K_GEMV || plan.kernel == p0k::K_GEMV_MF) {
     const uint32_t tiles = (a->N + 127) / 128;
     if (plan.S > 1) {
       if (tiles > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "gemm: N too large for the decode workspace");
@@ -337,7 +337,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
         c->ws_part_bytes = need;
       }
     }
-    e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream);
+    e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF);
   } else {
     e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, plan.bm, plan.bn, c->stream);
   }

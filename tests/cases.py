@@ -74,7 +74,7 @@ class Case:
         a = self.args(lambda n: h[n])
         if weights is None:
             import p0k
-            weights = oracle.CPU_WEIGHTS if p0k.select_tile(a)["kernel"] == "gemv" else oracle.KERNEL_WEIGHTS
+            weights = oracle.CPU_WEIGHTS if p0k.select_tile(a)["kernel"].startswith("gemv") else oracle.KERNEL_WEIGHTS
         oracle.gemm(a, m0, m1, weights)
         return h[self.out]
 

@@ -128,7 +128,9 @@ def test_conv3_frame_window_checked():
 
 
 def test_kernel_choice():
-    assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv"
+    assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv"
+    assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
+    assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma"
     c = make_conv3_case(T=1, H=2, W=2)                     # M = 4, a convolution: always the MFMA kernel
     assert p0k.select_tile(host_args(c))["kernel"] == "mfma"

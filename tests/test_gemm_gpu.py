@@ -77,7 +77,7 @@ EPIS = [
 ]
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 70])
+@pytest.mark.parametrize("M", [1, 2, 4, 16, 70])
 @pytest.mark.parametrize("enc", ["f16", "q4g32a.t64", "q8g64s.t64"])
 @pytest.mark.parametrize("xmode,epi,kw", EPIS, ids=[f"{x}-{e}-{i}" for i, (x, e, _) in enumerate(EPIS)])
 def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw):
@@ -86,7 +86,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw):
     K = 256
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if M <= 16 else "mfma")
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if M == 1 else "gemv_mfma" if M <= 16 else "mfma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
@@ -112,7 +112,7 @@ def _adversarial_q8(rows, K, seed):
 
 
 @pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
-@pytest.mark.parametrize("path", ["gemv", "mfma"])
+@pytest.mark.parametrize("path", ["gemv", "gemv_mfma", "mfma"])
 def test_dequant_bit_exact(dev, enc, path):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
@@ -122,7 +122,7 @@ def test_dequant_bit_exact(dev, enc, path):
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
     dw = dev.upload(wb)
     try:
-        M = 16 if path == "gemv" else K
+        M = {"gemv": 1, "gemv_mfma": 16, "mfma": K}[path]
         got = np.zeros((K, rows), np.uint16)
         for k0 in range(0, K, M):
             X = np.zeros((M, K), np.float32)
