@@ -111,6 +111,31 @@ typedef struct p0k_rowstats_args {
   float *st_buf; uint32_t st_off; uint64_t st_size;
 } p0k_rowstats_args;
 
+/* pixstats (src/ops/video.js:301-321): R[ro + v] = 1 / sqrt(sum_c x[v][c]^2 / C + eps) for voxels v < V of an f16
+ * [V][C] tensor (C % 4 == 0) - the per-voxel scale the conv3 `pn` prologue reads. eps 0 = the reference's 1e-8. */
+typedef struct p0k_pixstats_args {
+  uint32_t struct_size;
+  const void *x_buf; uint64_t x_off, x_size;  /* x_off in bytes */
+  uint32_t V, C; float eps;
+  float *r_buf; uint32_t ro; uint64_t r_size;  /* ro in floats */
+} p0k_pixstats_args;
+
+/* GroupNorm(32) statistics (src/ops/misc.js:50-109) of an HWC f16 tensor x [pix][C], C a power of two in 32..512:
+ *   partial rows (gnPartial): part[(wg_off + w) * 32 + g] = (n, mean, M2, 0) per 64-pixel chunk w and group g
+ *   finalize (gnFinalize):    merge nwg rows -> ab[ab_off + c] = gamma[c] / sqrt(M2 / n + eps),
+ *                             ab[ab_off + C + c] = beta[c] - mean * ab[ab_off + c]   (GN(x) = a x + b per channel)
+ * gamma / beta are fp32 vectors in gb_buf at byte offsets g_off / b_off (the reference's gb.gOff / gb.bOff).
+ * eps 0 = the reference's 1e-6. */
+typedef struct p0k_gn_args {
+  uint32_t struct_size;
+  const void *x_buf; uint64_t x_off, x_size;
+  uint32_t pix, C;
+  float *part_buf; uint32_t wg_off, nwg; uint64_t part_size;   /* nwg: rows to merge (finalize); 0 = ceil(pix / 64) */
+  const float *gb_buf; uint64_t g_off, b_off, gb_size;
+  float *ab_buf; uint32_t ab_off; uint64_t ab_size;             /* ab_off in floats */
+  float eps;
+} p0k_gn_args;
+
 typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM, 1 = GEMV (M = 1), 2 = MFMA GEMV (2 <= M <= 16) */
   p0k_tile;
 
@@ -150,6 +175,17 @@ double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the r
 int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use */
 int p0k_rowstats_check(const p0k_rowstats_args *a);
 int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
+
+/* pixstats(gpu, a)               src/ops/video.js:317  */
+int p0k_pixstats(p0k_ctx *ctx, const p0k_pixstats_args *a);
+/* gnPartBytes(pix)               src/ops/misc.js:92    bytes of the partial rows of pix pixels */
+uint64_t p0k_gn_part_bytes(uint32_t pix);
+/* gnPartial(gpu, a) -> nwg       src/ops/misc.js:94    */
+int p0k_gn_partial(p0k_ctx *ctx, const p0k_gn_args *a, uint32_t *nwg_out);
+/* gnFinalize(gpu, a)             src/ops/misc.js:101   */
+int p0k_gn_finalize(p0k_ctx *ctx, const p0k_gn_args *a);
+/* groupnormStats(gpu, a)         src/ops/misc.js:106   partial rows of the whole tensor, then finalize */
+int p0k_groupnorm_stats(p0k_ctx *ctx, const p0k_gn_args *a);
 
 /* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
  *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */

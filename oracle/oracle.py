@@ -50,6 +50,9 @@ def lib():
             ("or_rowstats", [C.POINTER(p0k.RowstatsArgs)], I),
             ("or_cpu_gemm", [P, P, I, I, I, P], None),
             ("or_cpu_conv3", [P, P, I, I, I, I, I, P], None),
+            ("or_pixstats", [P, C.c_uint32, C.c_uint32, C.c_float, P], None),
+            ("or_gn_partial", [P, C.c_uint32, C.c_uint32, P], None),
+            ("or_gn_finalize", [P, C.c_uint32, C.c_uint32, C.c_float, P, P, P], None),
         ]:
             fn = getattr(L, name)
             fn.argtypes, fn.restype = args, res
@@ -164,3 +167,29 @@ def cpu_conv3(X, Wt, T, H, W, Cc, N):
     Y = np.empty(T * H * W * N, np.float32)
     lib().or_cpu_conv3(_p(X), _p(Wt), T, H, W, Cc, N, _p(Y))
     return Y
+
+
+def pixstats(x16, V, Cc, eps=1e-8):
+    """R[v] = 1 / sqrt(sum_c x^2 / C + eps) (src/ops/video.js:301-321); x16: fp16 bits [V][C]."""
+    x16 = np.ascontiguousarray(x16, np.uint16)
+    r = np.empty(V, np.float32)
+    lib().or_pixstats(_p(x16), V, Cc, eps, _p(r))
+    return r
+
+
+def gn_partial(x16, pix, Cc):
+    """partial rows [ceil(pix / 64)][32][(n, mean, M2, 0)] (src/ops/misc.js:50-76)."""
+    x16 = np.ascontiguousarray(x16, np.uint16)
+    part = np.zeros(((pix + 63) // 64) * 32 * 4, np.float32)
+    lib().or_gn_partial(_p(x16), pix, Cc, _p(part))
+    return part
+
+
+def gn_finalize(part, nwg, Cc, gamma, beta, eps=1e-6):
+    """(a[C], b[C]) with GN(x) = a x + b (src/ops/misc.js:77-91)."""
+    part = np.ascontiguousarray(part, np.float32)
+    gamma = np.ascontiguousarray(gamma, np.float32)
+    beta = np.ascontiguousarray(beta, np.float32)
+    ab = np.empty(2 * Cc, np.float32)
+    lib().or_gn_finalize(_p(part), nwg, Cc, eps, _p(gamma), _p(beta), _p(ab))
+    return ab

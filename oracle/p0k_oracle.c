@@ -11,6 +11,9 @@
  *                        numpy formulation of the reference formulas, plus invariants (rotation preserves norm, V
  *                        passes unchanged, conv3 chunks == whole clip, conv3 == textbook cross-correlation)
  *   or_rowstats          numpy mean / variance
+ *   or_pixstats          src/ops/video.js:301-321 (PixelNorm scale per voxel)
+ *   or_gn_partial        src/ops/misc.js:50-76 (per 64-pixel chunk: n, mean, M2 of each of 32 groups)
+ *   or_gn_finalize       src/ops/misc.js:77-91 (Chan's merge of the chunks in order; a = gamma rstd, b = beta - mean a)
  */
 #include "p0k_oracle.h"
 
@@ -442,4 +445,53 @@ void or_cpu_conv3(const float *X, const float *Wt, int T, int H, int W, int C, i
               }
           Y[(((int64_t)t * H + y) * W + x) * N + n] = (float)s;
         }
+}
+
+/* ------------------------------------------------------------------ pixstats / GroupNorm statistics */
+void or_pixstats(const uint16_t *x, uint32_t V, uint32_t C, float eps, float *r) {
+  for (uint32_t v = 0; v < V; v++) {
+    double s = 0;
+    for (uint32_t c = 0; c < C; c++) { double t = or_h2f(x[(uint64_t)v * C + c]); s += t * t; }
+    r[v] = (float)(1.0 / sqrt(s / C + (double)eps));
+  }
+}
+
+void or_gn_partial(const uint16_t *x, uint32_t pix, uint32_t C, float *part) {
+  const uint32_t cpg = C / 32, nwg = (pix + 63) / 64;
+  for (uint32_t w = 0; w < nwg; w++) {
+    const uint32_t p0 = w * 64, np = pix - p0 < 64 ? pix - p0 : 64;
+    for (uint32_t g = 0; g < 32; g++) {
+      double s = 0, m2 = 0, n = (double)np * cpg;
+      for (uint32_t p = p0; p < p0 + np; p++)
+        for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) s += or_h2f(x[(uint64_t)p * C + c]);
+      double mean = s / (n > 1 ? n : 1);
+      for (uint32_t p = p0; p < p0 + np; p++)
+        for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) { double d = or_h2f(x[(uint64_t)p * C + c]) - mean; m2 += d * d; }
+      float *q = part + ((uint64_t)w * 32 + g) * 4;
+      q[0] = (float)n; q[1] = (float)mean; q[2] = (float)m2; q[3] = 0.0f;
+    }
+  }
+}
+
+void or_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma, const float *beta,
+                    float *ab) {
+  const uint32_t cpg = C / 32;
+  for (uint32_t g = 0; g < 32; g++) {
+    double n = 0, mean = 0, m2 = 0;
+    for (uint32_t w = 0; w < nwg; w++) {
+      const float *q = part + ((uint64_t)w * 32 + g) * 4;
+      if (q[0] > 0) {
+        double nn = n + q[0], d = q[1] - mean;
+        mean += d * (q[0] / nn);
+        m2 += q[2] + d * d * (n * q[0] / nn);
+        n = nn;
+      }
+    }
+    double rs = 1.0 / sqrt(m2 / (n > 1 ? n : 1) + (double)eps);
+    for (uint32_t c = g * cpg; c < (g + 1) * cpg; c++) {
+      double a = gamma[c] * rs;
+      ab[c] = (float)a;
+      ab[C + c] = (float)(beta[c] - mean * a);
+    }
+  }
 }

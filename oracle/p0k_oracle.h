@@ -48,6 +48,11 @@ int or_rowstats(const p0k_rowstats_args *a);
 /* the test suite's plain CPU references (test/kernels.test.js:29, :52-65), fp64 accumulation */
 void or_cpu_gemm(const float *X, const float *W, int M, int N, int K, float *Y);
 void or_cpu_conv3(const float *X, const float *Wt, int T, int H, int W, int C, int N, float *Y);
+/* pixstats / GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109) */
+void or_pixstats(const uint16_t *x, uint32_t V, uint32_t C, float eps, float *r);
+void or_gn_partial(const uint16_t *x, uint32_t pix, uint32_t C, float *part);
+void or_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma, const float *beta,
+                    float *ab);
 
 #ifdef __cplusplus
 }

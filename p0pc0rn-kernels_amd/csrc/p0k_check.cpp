@@ -277,4 +277,39 @@ int prepare_rowstats(const p0k_rowstats_args *a, std::string *err) {
   return P0K_OK;
 }
 
+int prepare_pixstats(const p0k_pixstats_args *a, std::string *err) {
+  NEED(a != nullptr, "pixstats: no arguments");
+  NEED(a->struct_size == sizeof(p0k_pixstats_args), "pixstats: struct_size %u, this library expects %u", a->struct_size,
+       (unsigned)sizeof(p0k_pixstats_args));
+  NEED(a->x_buf && a->r_buf, "pixstats: missing x or r buffer");
+  NEED(a->C > 0 && a->C % 4 == 0, "pixstats: C must be a positive multiple of 4");
+  NEED(a->x_off % 2 == 0, "pixstats: x.off must be a multiple of 2 bytes");
+  FITS("x", a->x_off + (uint64_t)a->V * a->C * 2, a->x_size);
+  FITS("r", ((uint64_t)a->ro + a->V) * 4, a->r_size);
+  return P0K_OK;
+}
+
+int prepare_gn(const p0k_gn_args *a, int what, std::string *err) {
+  NEED(a != nullptr, "groupnorm: no arguments");
+  NEED(a->struct_size == sizeof(p0k_gn_args), "groupnorm: struct_size %u, this library expects %u", a->struct_size,
+       (unsigned)sizeof(p0k_gn_args));
+  NEED(a->C >= 32 && a->C <= 512 && (a->C & (a->C - 1)) == 0, "groupnorm: C must be a power of two in 32..512");
+  NEED(a->part_buf, "groupnorm: missing part buffer");
+  if (what & 1) {
+    NEED(a->x_buf, "groupnorm: missing x buffer");
+    NEED(a->x_off % 2 == 0, "groupnorm: x.off must be a multiple of 2 bytes");
+    FITS("x", a->x_off + (uint64_t)a->pix * a->C * 2, a->x_size);
+    FITS("part", ((uint64_t)a->wg_off + (a->pix + 63) / 64) * 512, a->part_size);
+  }
+  if (what & 2) {
+    NEED(a->gb_buf && a->ab_buf, "groupnorm: missing gb or ab buffer");
+    NEED(a->g_off % 4 == 0 && a->b_off % 4 == 0, "groupnorm: gamma / beta offsets must be multiples of 4 bytes");
+    const uint64_t nwg = a->nwg ? a->nwg : (a->pix + 63) / 64;
+    FITS("part", nwg * 512, a->part_size);
+    FITS("gb", (a->g_off > a->b_off ? a->g_off : a->b_off) + (uint64_t)a->C * 4, a->gb_size);
+    FITS("ab", ((uint64_t)a->ab_off + 2ull * a->C) * 4, a->ab_size);
+  }
+  return P0K_OK;
+}
+
 }  // namespace p0k

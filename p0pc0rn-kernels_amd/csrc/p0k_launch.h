@@ -19,4 +19,9 @@ hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *c
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);
+// pixstats and GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109)
+hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, float *r, hipStream_t s);
+hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);
+hipError_t launch_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma,
+                              const float *beta, float *ab, hipStream_t s);
 }  // namespace p0k

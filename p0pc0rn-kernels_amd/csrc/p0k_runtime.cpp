@@ -370,6 +370,63 @@ int p0k_rowstats(p0k_ctx *c, const p0k_rowstats_args *a) {
   return P0K_OK;
 }
 
+// ------------------------------------------------------------------------------------------------ pixstats / GroupNorm
+static int check_live(p0k_ctx *c, const void *buf, uint64_t size, const char *op, const char *what) {
+  std::lock_guard<std::mutex> lk(c->mu);
+  auto it = c->live.find(const_cast<void *>(buf));
+  if (it == c->live.end()) return set_err(P0K_E_ARG, std::string(op) + ": " + what + " is not a live buffer of this context");
+  if (size > it->second) return set_err(P0K_E_ARG, std::string(op) + ": " + what + " size exceeds its allocation");
+  return P0K_OK;
+}
+
+int p0k_pixstats(p0k_ctx *c, const p0k_pixstats_args *a) {
+  if (!c) return set_err(P0K_E_ARG, "pixstats: NULL context");
+  std::string err;
+  int r = p0k::prepare_pixstats(a, &err);
+  if (r) return set_err(r, err);
+  if ((r = check_live(c, a->x_buf, a->x_size, "pixstats", "x")) || (r = check_live(c, a->r_buf, a->r_size, "pixstats", "r")))
+    return r;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_pixstats((const uint8_t *)a->x_buf + a->x_off, a->V, a->C, a->eps != 0.0f ? a->eps : 1e-8f,
+                                      a->r_buf + a->ro, c->stream);
+  if (e != hipSuccess) return hip_err(e, "pixstats launch");
+  return P0K_OK;
+}
+
+uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
+
+static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {
+  if (!c) return set_err(P0K_E_ARG, "groupnorm: NULL context");
+  std::string err;
+  int r = p0k::prepare_gn(a, what, &err);
+  if (r) return set_err(r, err);
+  if ((r = check_live(c, a->part_buf, a->part_size, "groupnorm", "part"))) return r;
+  if ((what & 1) && (r = check_live(c, a->x_buf, a->x_size, "groupnorm", "x"))) return r;
+  if ((what & 2) && ((r = check_live(c, a->gb_buf, a->gb_size, "groupnorm", "gb")) ||
+                     (r = check_live(c, a->ab_buf, a->ab_size, "groupnorm", "ab"))))
+    return r;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  const uint32_t nwg = (a->pix + 63) / 64;
+  if (what & 1) {
+    hipError_t e = p0k::launch_gn_partial((const uint8_t *)a->x_buf + a->x_off, a->pix, a->C, a->part_buf, a->wg_off, c->stream);
+    if (e != hipSuccess) return hip_err(e, "groupnorm partial launch");
+  }
+  if (what & 2) {
+    const uint32_t n = (what & 1) ? a->wg_off + nwg : (a->nwg ? a->nwg : nwg);
+    const float *gb = a->gb_buf;
+    hipError_t e = p0k::launch_gn_finalize(a->part_buf, n, a->C, a->eps != 0.0f ? a->eps : 1e-6f,
+                                           (const float *)((const uint8_t *)gb + a->g_off),
+                                           (const float *)((const uint8_t *)gb + a->b_off), a->ab_buf + a->ab_off, c->stream);
+    if (e != hipSuccess) return hip_err(e, "groupnorm finalize launch");
+  }
+  if (nwg_out) *nwg_out = nwg;
+  return P0K_OK;
+}
+
+int p0k_gn_partial(p0k_ctx *c, const p0k_gn_args *a, uint32_t *nwg_out) { return gn_run(c, a, 1, nwg_out); }
+int p0k_gn_finalize(p0k_ctx *c, const p0k_gn_args *a) { return gn_run(c, a, 2, nullptr); }
+int p0k_groupnorm_stats(p0k_ctx *c, const p0k_gn_args *a) { return gn_run(c, a, 3, nullptr); }
+
 // ------------------------------------------------------------------------------------------------ graphs
 struct p0k_graph { hipGraph_t graph; hipGraphExec_t exec; };
 

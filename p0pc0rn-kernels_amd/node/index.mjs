@@ -4,6 +4,7 @@
 //   createGpu / Gpu (src/core/gpu.js:15, :30)      buffer, upload, read, free, done, poolStats, drainPool, freeAll, describe
 //   gemm(gpu, args) (src/ops/gemm.js:268)          same argument object, same synchronous argument errors, returns 2MNK
 //   rowstats(gpu, args) (src/ops/misc.js:37)       mean / rstd per row, the statistics the rms and lnmod prologues read
+//   pixstats (src/ops/video.js:317), gnPartBytes / gnPartial / gnFinalize / groupnormStats (src/ops/misc.js:92-109)
 //   defaultTune / calibrate / tuneEntry / TUNE_TABLE (src/core/tune.js:18-58)
 //   loadWeights / uploadWeights (src/weights.js:10, :28)
 //   f2h / h2f / toF16 / fromF16 (src/core/gpu.js:276-299), packQ4 / packQ8 / packF16 (src/convert/encode.js:56-98)
@@ -241,6 +242,31 @@ function rowstats(gpu, a) {
   });
 }
 
+// ------------------------------------------------------------------ conv prologue statistics (src/ops/video.js, misc.js)
+/** pixstats(gpu, {x: {buf, off}, r: {buf}, V, C, eps = 1e-8, ro}): r[ro + v] = 1 / sqrt(mean_c x[v][c]^2 + eps) */
+function pixstats(gpu, a) {
+  call(addon().pixstats, gpu.ctx, { x_buf: ptrOf(a.x.buf), x_off: a.x.off || 0, x_size: sizeOf(a.x.buf), V: a.V, C: a.C,
+    eps: a.eps || 0, r_buf: ptrOf(a.r.buf), ro: a.ro || 0, r_size: sizeOf(a.r.buf) });
+}
+
+/** bytes of the GroupNorm partial rows of pix pixels */
+function gnPartBytes(pix) { return Math.ceil(pix / 64) * 512; }
+
+function gnDesc(a) {
+  const d = { pix: a.pix || 0, C: a.C, part_buf: ptrOf(a.part), part_size: sizeOf(a.part), wg_off: a.wgOff || 0,
+    nwg: a.nwg || 0, eps: a.eps || 0 };
+  if (a.x) Object.assign(d, { x_buf: ptrOf(a.x.buf), x_off: a.x.off || 0, x_size: a.x.size != null ? a.x.size + (a.x.off || 0) : sizeOf(a.x.buf) });
+  if (a.gb) Object.assign(d, { gb_buf: ptrOf(a.gb.buf), g_off: a.gb.gOff || 0, b_off: a.gb.bOff || 0, gb_size: sizeOf(a.gb.buf) });
+  if (a.ab) Object.assign(d, { ab_buf: ptrOf(a.ab.buf), ab_off: a.ab.off || 0, ab_size: sizeOf(a.ab.buf) });
+  return d;
+}
+/** gnPartial(gpu, {x, pix, C, part, wgOff}) -> rows written (ceil(pix / 64)) */
+function gnPartial(gpu, a) { return call(addon().gn, gpu.ctx, gnDesc(a), 1); }
+/** gnFinalize(gpu, {part, nwg, C, gb: {buf, gOff, bOff}, ab: {buf, off}, eps = 1e-6}) */
+function gnFinalize(gpu, a) { call(addon().gn, gpu.ctx, gnDesc(a), 2); }
+/** groupnormStats(gpu, {x, pix, C, part, gb, ab, eps}) */
+function groupnormStats(gpu, a) { call(addon().gn, gpu.ctx, gnDesc(a), 3); }
+
 // ------------------------------------------------------------------ tune (src/core/tune.js)
 /** per-device tile / accumulation choices; matched against gpu.info like the reference's table */
 const TUNE_TABLE = [
@@ -397,7 +423,7 @@ function encodedBytes(enc, rows, cols) {
 
 export {
   MB, GpuError, createGpu, Gpu, f2h, h2f, toF16, fromF16,
-  gemm, gemmPlan, gemmDesc, DEFAULT_TILE, rowstats,
+  gemm, gemmPlan, gemmDesc, DEFAULT_TILE, rowstats, pixstats, gnPartBytes, gnPartial, gnFinalize, groupnormStats,
   TUNE_TABLE, tuneEntry, defaultTune, calibrate,
   MANIFEST_FORMAT, loadWeights, uploadWeights,
   packQ4, packQ8, packF16, encodedBytes,

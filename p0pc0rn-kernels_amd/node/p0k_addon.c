@@ -4,7 +4,8 @@
  * every argument check happens in libp0k, whose message becomes the thrown Error's message.
  *
  * Exports: ctxCreate, ctxDestroy, deviceInfo, alloc, free, upload, download, copy, sync, poolStats, drainPool,
- *          gemm, gemmCheck, selectTile, rowstats, packQ4, packQ8, packF16, tensorBytes, lastError, abiVersion
+ *          gemm, gemmCheck, selectTile, rowstats, pixstats, gn, gnPartBytes, packQ4, packQ8, packF16, tensorBytes,
+ *          lastError, abiVersion
  * (N-API version 6 or later: BigInt support; Node 12.17+).
  */
 #define NAPI_VERSION 6
@@ -374,6 +375,64 @@ static napi_value rowstats(napi_env env, napi_callback_info info) {   /* (ctx, {
   return undef(env);
 }
 
+/* ------------------------------------------------------------------ pixstats / GroupNorm statistics */
+#define FIELD(obj, name, dst, ...)                                                        \
+  do {                                                                                    \
+    uint64_t t_;                                                                          \
+    if (!field_u64(env, obj, name, &t_)) { napi_throw_type_error(env, NULL, "field " name); return NULL; } \
+    dst = __VA_ARGS__ t_;                                                                 \
+  } while (0)
+
+static napi_value pixstats(napi_env env, napi_callback_info info) {   /* (ctx, {x_buf, x_off, x_size, V, C, eps, r_buf, ro, r_size}) */
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  napi_value o = argv[1];
+  p0k_pixstats_args a;
+  memset(&a, 0, sizeof a);
+  a.struct_size = sizeof a;
+  FIELD(o, "x_buf", a.x_buf, (const void *)(uintptr_t));
+  FIELD(o, "x_off", a.x_off, ); FIELD(o, "x_size", a.x_size, ); FIELD(o, "V", a.V, ); FIELD(o, "C", a.C, );
+  FIELD(o, "r_buf", a.r_buf, (float *)(uintptr_t));
+  FIELD(o, "ro", a.ro, ); FIELD(o, "r_size", a.r_size, );
+  if (!field_f32(env, o, "eps", &a.eps)) { napi_throw_type_error(env, NULL, "field eps"); return NULL; }
+  int r = p0k_pixstats(get_ctx(env, argv[0]), &a);
+  if (r) return throw_p0k(env, r);
+  return undef(env);
+}
+
+static napi_value gn(napi_env env, napi_callback_info info) {   /* (ctx, desc, what 1 | 2 | 3) -> partial rows written */
+  napi_value argv[3];
+  if (!get_args(env, info, 3, argv)) return NULL;
+  napi_value o = argv[1];
+  int32_t what = 3;
+  napi_get_value_int32(env, argv[2], &what);
+  p0k_gn_args a;
+  memset(&a, 0, sizeof a);
+  a.struct_size = sizeof a;
+  FIELD(o, "x_buf", a.x_buf, (const void *)(uintptr_t));
+  FIELD(o, "x_off", a.x_off, ); FIELD(o, "x_size", a.x_size, ); FIELD(o, "pix", a.pix, ); FIELD(o, "C", a.C, );
+  FIELD(o, "part_buf", a.part_buf, (float *)(uintptr_t));
+  FIELD(o, "wg_off", a.wg_off, ); FIELD(o, "nwg", a.nwg, ); FIELD(o, "part_size", a.part_size, );
+  FIELD(o, "gb_buf", a.gb_buf, (const float *)(uintptr_t));
+  FIELD(o, "g_off", a.g_off, ); FIELD(o, "b_off", a.b_off, ); FIELD(o, "gb_size", a.gb_size, );
+  FIELD(o, "ab_buf", a.ab_buf, (float *)(uintptr_t));
+  FIELD(o, "ab_off", a.ab_off, ); FIELD(o, "ab_size", a.ab_size, );
+  if (!field_f32(env, o, "eps", &a.eps)) { napi_throw_type_error(env, NULL, "field eps"); return NULL; }
+  p0k_ctx *ctx = get_ctx(env, argv[0]);
+  uint32_t nwg = 0;
+  int r = what == 1 ? p0k_gn_partial(ctx, &a, &nwg) : what == 2 ? p0k_gn_finalize(ctx, &a) : p0k_groupnorm_stats(ctx, &a);
+  if (r) return throw_p0k(env, r);
+  return mk_num(env, nwg);
+}
+
+static napi_value gnPartBytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return NULL;
+  uint64_t pix;
+  if (!to_u64(env, argv[0], &pix)) return NULL;
+  return mk_num(env, (double)p0k_gn_part_bytes((uint32_t)pix));
+}
+
 /* ------------------------------------------------------------------ encoders (host) */
 static napi_value pack_q(napi_env env, napi_callback_info info, int enc) {   /* (Float32Array W, rows, K, deq?) -> Uint8Array */
   napi_value argv[4];
@@ -454,6 +513,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"poolStats", poolStats}, {"drainPool", drainPool}, {"gemm", gemm}, {"gemmCheck", gemmCheck},
       {"selectTile", selectTile}, {"rowstats", rowstats}, {"packQ4", packQ4}, {"packQ8", packQ8},
       {"packF16", packF16}, {"tensorBytes", tensorBytes}, {"lastError", lastError}, {"abiVersion", abiVersion},
+      {"pixstats", pixstats}, {"gn", gn}, {"gnPartBytes", gnPartBytes},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
     napi_value f;

@@ -64,6 +64,27 @@ class RowstatsArgs(C.Structure):
     ]
 
 
+class PixstatsArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("x_buf", C.c_void_p), ("x_off", C.c_uint64), ("x_size", C.c_uint64),
+        ("V", C.c_uint32), ("C", C.c_uint32), ("eps", C.c_float),
+        ("r_buf", C.c_void_p), ("ro", C.c_uint32), ("r_size", C.c_uint64),
+    ]
+
+
+class GnArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("x_buf", C.c_void_p), ("x_off", C.c_uint64), ("x_size", C.c_uint64),
+        ("pix", C.c_uint32), ("C", C.c_uint32),
+        ("part_buf", C.c_void_p), ("wg_off", C.c_uint32), ("nwg", C.c_uint32), ("part_size", C.c_uint64),
+        ("gb_buf", C.c_void_p), ("g_off", C.c_uint64), ("b_off", C.c_uint64), ("gb_size", C.c_uint64),
+        ("ab_buf", C.c_void_p), ("ab_off", C.c_uint32), ("ab_size", C.c_uint64),
+        ("eps", C.c_float),
+    ]
+
+
 class Tile(C.Structure):
     _fields_ = [("bm", C.c_uint32), ("bn", C.c_uint32), ("kernel", C.c_int32)]
 
@@ -83,6 +104,7 @@ EXPORTS = [
     "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
+    "p0k_pixstats", "p0k_gn_part_bytes", "p0k_gn_partial", "p0k_gn_finalize", "p0k_groupnorm_stats",
     "p0k_event_create", "p0k_event_record", "p0k_event_elapsed_ms", "p0k_event_destroy",
     "p0k_tensor_bytes", "p0k_pack_q4", "p0k_pack_q8", "p0k_pack_f16",
     "p0k_graph_begin", "p0k_graph_end", "p0k_graph_launch", "p0k_graph_destroy",
@@ -111,6 +133,9 @@ def lib():
             "p0k_gemm_flops": ([C.POINTER(GemmArgs)], C.c_double),
             "p0k_select_tile": ([C.POINTER(GemmArgs), C.POINTER(Tile)], I),
             "p0k_rowstats_check": ([C.POINTER(RowstatsArgs)], I), "p0k_rowstats": ([P, C.POINTER(RowstatsArgs)], I),
+            "p0k_pixstats": ([P, C.POINTER(PixstatsArgs)], I), "p0k_gn_part_bytes": ([C.c_uint32], U64),
+            "p0k_gn_partial": ([P, C.POINTER(GnArgs), C.POINTER(C.c_uint32)], I),
+            "p0k_gn_finalize": ([P, C.POINTER(GnArgs)], I), "p0k_groupnorm_stats": ([P, C.POINTER(GnArgs)], I),
             "p0k_event_create": ([P, C.POINTER(P)], I), "p0k_event_record": ([P, P], I),
             "p0k_event_elapsed_ms": ([P, P, C.POINTER(C.c_float)], I), "p0k_event_destroy": ([P], None),
             "p0k_tensor_bytes": ([I, C.c_uint32, C.c_uint32], U64),
@@ -300,6 +325,46 @@ class Device:
         r.mode, r.eps = (1 if mode == "rms" else 0), eps
         r.st_buf, r.st_off, r.st_size = st.ptr, st_off, st.size
         _chk(lib().p0k_rowstats(self.ctx, C.byref(r)))
+
+    def pixstats(self, x, V, Cc, r, eps=0.0, ro=0, x_off=0):
+        """pixstats(gpu, {x, r, V, C, eps, ro}) of src/ops/video.js:317."""
+        a = PixstatsArgs()
+        a.struct_size = C.sizeof(PixstatsArgs)
+        a.x_buf, a.x_off, a.x_size = x.ptr, x_off, x.size
+        a.V, a.C, a.eps = V, Cc, eps
+        a.r_buf, a.ro, a.r_size = r.ptr, ro, r.size
+        _chk(lib().p0k_pixstats(self.ctx, C.byref(a)))
+
+    @staticmethod
+    def _gn(x, pix, Cc, part, gb=None, g_off=0, b_off=0, ab=None, ab_off=0, eps=0.0, wg_off=0, nwg=0, x_off=0):
+        a = GnArgs()
+        a.struct_size = C.sizeof(GnArgs)
+        if x is not None:
+            a.x_buf, a.x_off, a.x_size = x.ptr, x_off, x.size
+        a.pix, a.C = pix, Cc
+        a.part_buf, a.wg_off, a.nwg, a.part_size = part.ptr, wg_off, nwg, part.size
+        if gb is not None:
+            a.gb_buf, a.g_off, a.b_off, a.gb_size = gb.ptr, g_off, b_off, gb.size
+        if ab is not None:
+            a.ab_buf, a.ab_off, a.ab_size = ab.ptr, ab_off, ab.size
+        a.eps = eps
+        return a
+
+    def gn_partial(self, x, pix, Cc, part, wg_off=0, x_off=0):
+        """gnPartial(gpu, {x, pix, C, part, wgOff}) of src/ops/misc.js:94; returns the number of partial rows."""
+        n = C.c_uint32()
+        _chk(lib().p0k_gn_partial(self.ctx, C.byref(self._gn(x, pix, Cc, part, wg_off=wg_off, x_off=x_off)), C.byref(n)))
+        return n.value
+
+    def gn_finalize(self, part, nwg, Cc, gb, g_off, b_off, ab, ab_off=0, eps=0.0):
+        """gnFinalize(gpu, {part, nwg, C, gb: {buf, gOff, bOff}, ab: {buf, off}, eps}) of src/ops/misc.js:101."""
+        a = self._gn(None, 0, Cc, part, gb, g_off, b_off, ab, ab_off, eps, nwg=nwg)
+        _chk(lib().p0k_gn_finalize(self.ctx, C.byref(a)))
+
+    def groupnorm_stats(self, x, pix, Cc, part, gb, g_off, b_off, ab, ab_off=0, eps=0.0):
+        """groupnormStats(gpu, a) of src/ops/misc.js:106."""
+        a = self._gn(x, pix, Cc, part, gb, g_off, b_off, ab, ab_off, eps)
+        _chk(lib().p0k_groupnorm_stats(self.ctx, C.byref(a)))
 
     # -- events on the context's stream
     def event(self):

@@ -4,6 +4,7 @@
 //   run_case.mjs gemm <dir>   GPU: spec.json (a reference gemm argument object with buffer NAMES) + <name>.bin buffers;
 //                             createGpu → upload → gemm → read → <out>_gpu.bin
 //   run_case.mjs weights <dir> GPU: loadWeights on a converted-model folder, then gemm with model.tensor(...)
+//   run_case.mjs stats <dir>  GPU: pixstats and groupnormStats
 'use strict';
 import { readFileSync, writeFileSync } from 'fs';
 import { join } from 'path';
@@ -91,5 +92,19 @@ async function weights() {
   model.free(); g.free(x); g.free(y); await g.done(); g.destroy();
 }
 
-const run = { host, gemm: gemmCase, weights }[mode];
+async function stats() {
+  const spec = JSON.parse(readFileSync(join(dir, 'spec.json'), 'utf8'));
+  const g = await p0k.createGpu();
+  const x = g.upload(bin('x.bin')), r = g.buffer(spec.V * 4);
+  p0k.pixstats(g, { x: { buf: x }, r: { buf: r }, V: spec.V, C: spec.C });
+  put('r_gpu.f32', new Float32Array(await g.read(r)));
+  const gx = g.upload(bin('gx.bin')), gb = g.upload(bin('gb.bin'));
+  const part = g.buffer(p0k.gnPartBytes(spec.pix)), ab = g.buffer(spec.GC * 8);
+  p0k.groupnormStats(g, { x: { buf: gx }, pix: spec.pix, C: spec.GC, part, gb: { buf: gb, gOff: 0, bOff: spec.GC * 4 }, ab: { buf: ab } });
+  put('ab_gpu.f32', new Float32Array(await g.read(ab)));
+  [x, r, gx, gb, part, ab].forEach((b) => g.free(b));
+  await g.done(); g.destroy();
+}
+
+const run = { host, gemm: gemmCase, weights, stats }[mode];
 run().catch((e) => { console.error(e && e.stack || e); process.exit(1); });

@@ -149,3 +149,23 @@ def test_shim_load_weights(tmp_path):
     case.bufs["w"], case.bufs["x"] = q4, x
     want = case.run_oracle()
     assert_close(y, want, fp16=True, what="loadWeights tensor gemm")
+
+
+@pytest.mark.gpu
+def test_shim_pixstats_and_groupnorm(tmp_path):
+    """pixstats (src/ops/video.js:317) and groupnormStats (src/ops/misc.js:106) through the shim."""
+    rng = np.random.default_rng(8)
+    V, Cc, pix, GC = 500, 128, 300, 64
+    x = oracle.f16_bits(rng.standard_normal(V * Cc).astype(np.float32))
+    gx = oracle.f16_bits(rng.standard_normal(pix * GC).astype(np.float32))
+    g, b = (1 + 0.1 * rng.standard_normal(GC)).astype(np.float32), (0.1 * rng.standard_normal(GC)).astype(np.float32)
+    x.tofile(str(tmp_path / "x.bin"))
+    gx.tofile(str(tmp_path / "gx.bin"))
+    np.concatenate([g, b]).tofile(str(tmp_path / "gb.bin"))
+    (tmp_path / "spec.json").write_text(json.dumps({"V": V, "C": Cc, "pix": pix, "GC": GC}))
+    node("stats", tmp_path)
+    r = np.fromfile(str(tmp_path / "r_gpu.f32"), np.float32)[:V]
+    np.testing.assert_allclose(r, oracle.pixstats(x, V, Cc, 1e-8), rtol=2e-6)
+    ab = np.fromfile(str(tmp_path / "ab_gpu.f32"), np.float32)[:2 * GC]
+    want = oracle.gn_finalize(oracle.gn_partial(gx, pix, GC), (pix + 63) // 64, GC, g, b, 1e-6)
+    np.testing.assert_allclose(ab, want, rtol=2e-6, atol=1e-7)
