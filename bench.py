@@ -64,9 +64,9 @@ def f16(a):
 class Workload:
     """Device buffers + a list of argument dicts (one per rotation copy) for one config."""
 
-    def __init__(self, name, desc, bound, flops, algo_bytes, M, args, bufs, extra=None):
+    def __init__(self, name, desc, bound, flops, algo_bytes, M, args, bufs, extra=None, kind="gemm"):
         self.name, self.desc, self.bound, self.flops, self.algo_bytes = name, desc, bound, flops, algo_bytes
-        self.M, self.args, self.bufs, self.extra = M, args, bufs, extra or {}
+        self.M, self.args, self.bufs, self.extra, self.kind = M, args, bufs, extra or {}, kind
 
 
 def decode_q4(dev, M, copies=None):
@@ -182,26 +182,47 @@ def conv3(dev):
                     2.0 * M * N * K, nbytes, M, args, [wt, x, y])
 
 
+def dit_attn(dev):
+    """the consumer of configs[3](a)'s heads output: attention over 24 heads of 128, 4096 tokens (no mask)."""
+    H, L = 24, 4096
+    r = rng(6)
+    q = dev.upload(f16(0.5 * r.standard_normal(H * L * 128)))
+    k = dev.upload(f16(0.5 * r.standard_normal(H * L * 128)))
+    v = dev.upload(f16(r.standard_normal(H * L * 128)))
+    o = dev.buffer(L * H * 128 * 2)
+    args = [{"q": {"buf": q}, "k": {"buf": k}, "v": {"buf": v}, "o": {"buf": o}, "Lq": L, "Lk": L, "Hq": H, "Hkv": H}]
+    return Workload("dit_attention_24x4096", "attention, 24 heads of 128, 4096 queries x 4096 keys, no mask", "mfma",
+                    4.0 * L * L * 128 * H, 4 * H * L * 128 * 2, L, args, [q, k, v, o], kind="attn")
+
+
 BUILDERS = {
     "decode1": lambda d: decode_q4(d, 1), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
-    "prefill": prefill_q8, "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3,
+    "prefill": prefill_q8, "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
 }
 
 
 # ------------------------------------------------------------------------------------------------ timing
 def time_workload(dev, wl, steps, warmup):
-    structs = [p0k.gemm_args(a, dev.resolve) for a in wl.args]
     L = p0k.lib()
     import ctypes as C
+    if wl.kind == "attn":
+        structs = [p0k.attn_args(a, dev.resolve) for a in wl.args]
+        run = dev.attention_raw
+        for s in structs:
+            p0k._chk(L.p0k_attention_check(C.byref(s)))
+    else:
+        structs = [p0k.gemm_args(a, dev.resolve) for a in wl.args]
+        run = dev.gemm_raw
+        for s in structs:
+            p0k._chk(L.p0k_gemm_check(C.byref(s)))
     for s in structs:
-        p0k._chk(L.p0k_gemm_check(C.byref(s)))
-        dev.gemm_raw(s)                 # one eager call per shape first: sizes the workspace before capture
+        run(s)                          # one eager call per shape first: sizes the workspace before capture
     dev.done()
     if os.environ.get("P0K_BENCH_EAGER"):            # profiling: plain launches, no graph
         e0, e1 = dev.event(), dev.event()
         dev.record(e0)
         for i in range(steps):
-            dev.gemm_raw(structs[i % len(structs)])
+            run(structs[i % len(structs)])
         dev.record(e1)
         dev.done()
         ms = dev.elapsed_ms(e0, e1) / steps
@@ -213,7 +234,7 @@ def time_workload(dev, wl, steps, warmup):
     dev.graph_begin()
     try:
         for i in range(per_graph):
-            dev.gemm_raw(structs[i % len(structs)])
+            run(structs[i % len(structs)])
     finally:
         g = dev.graph_end()
     reps = max(1, -(-steps // per_graph))
@@ -325,6 +346,8 @@ def main():
     if not a.no_cpu:
         cache = {}
         for n, res in results.items():
+            if res["name"] not in CPU_SAMPLE:
+                continue
             cfg, rows = CPU_SAMPLE[res["name"]]
             whole = n == "decode1"                                       # the headline: time whole M=1 calls
             key = (cfg, rows, whole)

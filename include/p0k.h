@@ -136,6 +136,21 @@ typedef struct p0k_gn_args {
   float eps;
 } p0k_gn_args;
 
+/* attention(gpu, a) (src/ops/attention.js:168-201), head size 128: Q [Hq][Lq][128], K / V [Hkv][Lk][128] f16 (the
+ * `heads` epilogue's layout), O [Lq][ldo] f16 with head h at column h * 128. mode 0: no mask; 1: key j visible to query
+ * i iff j <= min(i, nvalid - 1); 2: j < nvalid. GQA: query head h reads kv head h / (Hq / Hkv). Zero fields take the
+ * reference's defaults: Lk = Lq, Hkv = Hq, nvalid = Lk, ldo = Hq * 128, scale = 1 / sqrt(128); cap > 0 soft-caps
+ * the scores to cap * tanh(s / cap). Offsets and sizes in bytes; q / k / v offsets 16-byte aligned, o 8-byte. */
+typedef struct p0k_attn_args {
+  uint32_t struct_size;
+  const void *q_buf; uint64_t q_off, q_size;
+  const void *k_buf; uint64_t k_off, k_size;
+  const void *v_buf; uint64_t v_off, v_size;
+  void *o_buf; uint64_t o_off, o_size; uint32_t ldo;
+  uint32_t Lq, Lk, Hq, Hkv, mode, nvalid;
+  float scale, cap;
+} p0k_attn_args;
+
 typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM, 1 = GEMV (M = 1), 2 = MFMA GEMV (2 <= M <= 16) */
   p0k_tile;
 
@@ -175,6 +190,11 @@ double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the r
 int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use */
 int p0k_rowstats_check(const p0k_rowstats_args *a);
 int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
+
+/* attention(gpu, a) -> 4 Lq Lk 128 Hq   src/ops/attention.js:168 */
+int p0k_attention_check(const p0k_attn_args *a);
+int p0k_attention(p0k_ctx *ctx, const p0k_attn_args *a);
+double p0k_attention_flops(const p0k_attn_args *a);
 
 /* pixstats(gpu, a)               src/ops/video.js:317  */
 int p0k_pixstats(p0k_ctx *ctx, const p0k_pixstats_args *a);

@@ -51,6 +51,7 @@ def lib():
             ("or_cpu_gemm", [P, P, I, I, I, P], None),
             ("or_cpu_conv3", [P, P, I, I, I, I, I, P], None),
             ("or_pixstats", [P, C.c_uint32, C.c_uint32, C.c_float, P], None),
+            ("or_attention", [P, P, P, P] + [C.c_uint32] * 7 + [C.c_float, C.c_float], None),
             ("or_gn_partial", [P, C.c_uint32, C.c_uint32, P], None),
             ("or_gn_finalize", [P, C.c_uint32, C.c_uint32, C.c_float, P, P, P], None),
         ]:
@@ -193,3 +194,14 @@ def gn_finalize(part, nwg, Cc, gamma, beta, eps=1e-6):
     ab = np.empty(2 * Cc, np.float32)
     lib().or_gn_finalize(_p(part), nwg, Cc, eps, _p(gamma), _p(beta), _p(ab))
     return ab
+
+
+def attention(q16, k16, v16, Lq, Lk, Hq, Hkv, mode=0, nvalid=None, scale=None, cap=0.0, ldo=None):
+    """cpuAttn (test/kernels.test.js:30-49), head size 128: fp16 bits in, O [Lq][ldo] fp16 bits out."""
+    ldo = ldo or Hq * 128
+    nvalid = Lk if nvalid is None else nvalid
+    scale = 1.0 / np.sqrt(128.0) if scale is None else scale
+    q16, k16, v16 = (np.ascontiguousarray(a, np.uint16) for a in (q16, k16, v16))
+    o = np.zeros(Lq * ldo, np.uint16)
+    lib().or_attention(_p(q16), _p(k16), _p(v16), _p(o), Lq, Lk, Hq, Hkv, ldo, mode, nvalid, scale, cap)
+    return o

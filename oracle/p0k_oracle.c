@@ -14,6 +14,7 @@
  *   or_pixstats          src/ops/video.js:301-321 (PixelNorm scale per voxel)
  *   or_gn_partial        src/ops/misc.js:50-76 (per 64-pixel chunk: n, mean, M2 of each of 32 groups)
  *   or_gn_finalize       src/ops/misc.js:77-91 (Chan's merge of the chunks in order; a = gamma rstd, b = beta - mean a)
+ *   or_attention         cpuAttn of test/kernels.test.js:30-49 (exact softmax in fp64), rounded to fp16 like the kernel
  */
 #include "p0k_oracle.h"
 
@@ -494,4 +495,36 @@ void or_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, cons
       ab[C + c] = (float)(beta[c] - mean * a);
     }
   }
+}
+
+/* ------------------------------------------------------------------ attention (cpuAttn, test/kernels.test.js:30-49) */
+void or_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, uint32_t Lq, uint32_t Lk,
+                  uint32_t Hq, uint32_t Hkv, uint32_t ldo, uint32_t mode, uint32_t nvalid, float scale, float cap) {
+  const uint32_t D = 128, grp = Hq / Hkv;
+  double *s = (double *)malloc(sizeof(double) * (Lk ? Lk : 1));
+  for (uint32_t h = 0; h < Hq; h++) {
+    const uint32_t kh = h / grp;
+    for (uint32_t i = 0; i < Lq; i++) {
+      double mx = -INFINITY;
+      for (uint32_t j = 0; j < Lk; j++) {
+        int vis = mode == 1 ? j <= (i < nvalid - 1 ? i : nvalid - 1) : mode == 2 ? j < nvalid : 1;
+        if (!vis) { s[j] = -INFINITY; continue; }
+        double a = 0;
+        for (uint32_t d = 0; d < D; d++)
+          a += (double)or_h2f(Q[((uint64_t)h * Lq + i) * D + d]) * or_h2f(K[((uint64_t)kh * Lk + j) * D + d]);
+        a *= scale;
+        if (cap > 0) a = cap * tanh(a / cap);
+        s[j] = a;
+        if (a > mx) mx = a;
+      }
+      double sum = 0;
+      for (uint32_t j = 0; j < Lk; j++) { s[j] = s[j] == -INFINITY ? 0 : exp(s[j] - mx); sum += s[j]; }
+      for (uint32_t d = 0; d < D; d++) {
+        double a = 0;
+        for (uint32_t j = 0; j < Lk; j++) if (s[j] != 0) a += s[j] * or_h2f(V[((uint64_t)kh * Lk + j) * D + d]);
+        O[(uint64_t)i * ldo + h * D + d] = or_f2h((float)(a / sum));
+      }
+    }
+  }
+  free(s);
 }

@@ -53,6 +53,9 @@ void or_pixstats(const uint16_t *x, uint32_t V, uint32_t C, float eps, float *r)
 void or_gn_partial(const uint16_t *x, uint32_t pix, uint32_t C, float *part);
 void or_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma, const float *beta,
                     float *ab);
+/* attention, head size 128 (cpuAttn, test/kernels.test.js:30-49) */
+void or_attention(const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O, uint32_t Lq, uint32_t Lk,
+                  uint32_t Hq, uint32_t Hkv, uint32_t ldo, uint32_t mode, uint32_t nvalid, float scale, float cap);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,194 @@
+// p0k_attention.hip — flash attention over the `heads` output of the QKV gemm (src/ops/attention.js:168-201), head
+// size 128, on gfx950 matrix cores.
+//
+//   Q [Hq][Lq][128] f16, K / V [Hkv][Lk][128] f16 (head-major, as the heads epilogue writes them), O [Lq][ldo] f16
+//   token-major at column h*128. Query head h reads kv head h / (Hq / Hkv). mode 0: no mask; 1: key j visible to query
+//   i iff j <= min(i, nvalid - 1); 2: j < nvalid. Scores s = scale * q.k (scale defaults to 1/sqrt(128)), optionally
+//   soft-capped to cap * tanh(s / cap); O = softmax(s) V with an exact online softmax in fp32.
+//
+// One workgroup (4 waves) owns 128 queries of one head; each wave owns 32 of them and keeps its Q rows in registers.
+// Everything is computed transposed, so that a lane owns ONE query and the softmax statistics stay in the lane:
+//   S^T (keys x queries) = K Q^T           v_mfma_f32_32x32x16_f16, A = K from LDS, B = Q^T from registers
+//   O^T (d x queries)   += V^T P           A = V^T from LDS, B = P = exp(S - m) from the S^T registers (fp16)
+// In the 32x32 layout lane l holds column l % 32 (its query) and 16 rows 8 (r/4) + 4 (l/32) + r%4, so a row maximum
+// or sum is a reduction over the lane's registers plus one exchange with lane l ^ 32. The 16 keys a lane contributes
+// to one P.V step are exactly the keys its S^T registers hold, so P never leaves the registers; V is staged in LDS
+// transposed ([d][key]) so those keys are two 8-byte reads. Keys come in tiles of 64 through double-buffered LDS (the
+// next tile's global loads are issued before this tile's MFMAs); both LDS tiles are XOR-swizzled so the 16-byte K reads
+// and the 8-byte V reads of a wave hit distinct banks.
+#include "p0k_device.h"
+#include "p0k_launch.h"
+
+namespace p0k {
+
+constexpr int AT_BQ = 128, AT_BK = 64, AT_NT = 256;
+
+__global__ __launch_bounds__(AT_NT) void k_attention(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) f16 sK[2][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ (key & 15)
+  __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ ((d >> 1) & 15)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, gh = lane >> 5, l32 = lane & 31;
+  const uint32_t h = blockIdx.y, hk = h / (p.Hq / p.Hkv);
+  const uint32_t q0 = blockIdx.x * AT_BQ, qw = q0 + wave * 32 + l32;
+  const uint32_t qc = qw < p.Lq ? qw : p.Lq - 1u;
+
+  // this lane's query row: 8 steps of 16 d, lane half gh holds d = 16 s + 8 gh .. + 7
+  f16x8 qf[8];
+  const uint16_t *qrow = p.Q + ((size_t)h * p.Lq + qc) * 128;
+#pragma unroll
+  for (int s = 0; s < 8; s++) qf[s] = *(const f16x8 *)(qrow + 16 * s + 8 * gh);
+
+  uint32_t kend = p.Lk;
+  if (p.mode == 1) {
+    const uint32_t last = q0 + AT_BQ - 1 < p.nvalid - 1 ? q0 + AT_BQ - 1 : p.nvalid - 1;
+    kend = p.Lk < last + 1 ? p.Lk : last + 1;
+  } else if (p.mode == 2) {
+    kend = p.Lk < p.nvalid ? p.Lk : p.nvalid;
+  }
+  // the keys this lane's query may see
+  uint32_t qlim = p.Lk;
+  if (p.mode == 1) qlim = (qc < p.nvalid - 1 ? qc : p.nvalid - 1) + 1;
+  else if (p.mode == 2) qlim = p.nvalid;
+  qlim = qlim < p.Lk ? qlim : p.Lk;
+  const uint32_t ntile = (kend + AT_BK - 1) / AT_BK;
+  const float sl2 = p.scale * 1.4426950408889634f;
+
+  const uint16_t *Kb = p.K + (size_t)hk * p.Lk * 128, *Vb = p.V + (size_t)hk * p.Lk * 128;
+  u32x4 kr[4], vr[4];
+  const uint32_t vkg = tid & 15, vdc = tid >> 4;        // V staging: keys 4 vkg .. + 3, d 8 vdc .. + 7
+  auto gload = [&](uint32_t t) {
+    const uint32_t k0 = t * AT_BK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = tid + AT_NT * i, key = k0 + c / 16;
+      kr[i] = *(const u32x4 *)(Kb + (size_t)(key < p.Lk ? key : p.Lk - 1u) * 128 + (c % 16) * 8);
+      const uint32_t vk = k0 + 4 * vkg + i;
+      vr[i] = *(const u32x4 *)(Vb + (size_t)(vk < p.Lk ? vk : p.Lk - 1u) * 128 + vdc * 8);
+    }
+  };
+  auto lstore = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = tid + AT_NT * i, key = c / 16, ch = c % 16;
+      *(u32x4 *)(sK[b] + key * 128 + ((ch ^ (key & 15u)) * 8)) = kr[i];
+    }
+    const uint16_t *v0 = (const uint16_t *)&vr[0], *v1 = (const uint16_t *)&vr[1], *v2 = (const uint16_t *)&vr[2],
+                   *v3 = (const uint16_t *)&vr[3];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t d = vdc * 8 + j;
+      *(u32x2 *)(sV[b] + d * AT_BK + ((vkg ^ ((d >> 1) & 15u)) * 4)) =
+          (u32x2){(uint32_t)v0[j] | ((uint32_t)v1[j] << 16), (uint32_t)v2[j] | ((uint32_t)v3[j] << 16)};
+    }
+  };
+
+  f32x16 oacc[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) oacc[i] = (f32x16){};
+  float m = -1.0e30f, l = 0.0f;
+
+  if (ntile) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (uint32_t t = 0; t < ntile; t++) {
+    const int b = t & 1;
+    const uint32_t k0 = t * AT_BK;
+    if (t + 1 < ntile) gload(t + 1);
+
+    // ---- S^T for keys k0 .. k0+63: two 32-key blocks
+    f32x16 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      sacc[kb] = (f32x16){};
+      const uint32_t key = 32 * kb + l32;
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const f16x8 a = *(const f16x8 *)(sK[b] + key * 128 + (((2 * s + gh) ^ (key & 15u)) * 8));
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sacc[kb], 0, 0, 0);
+      }
+    }
+    // ---- scale, cap, mask (log2 domain), row max over the 64 keys
+    if (p.cap > 0.0f) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) sacc[kb][r] = p.cap * tanhf(sacc[kb][r] * p.scale / p.cap) * 1.4426950408889634f;
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) sacc[kb] *= sl2;
+    }
+    const uint32_t kl = qlim > k0 ? qlim - k0 : 0u;           // keys of this tile the lane's query sees: [0, kl)
+    float mx = -1.0e30f;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t key = 32 * kb + 8 * (r >> 2) + 4 * gh + (r & 3);
+        const float v = key < kl ? sacc[kb][r] : -1.0e30f;
+        sacc[kb][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
+    m = mn;
+    float ps = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float v = sacc[kb][r];
+        const float e = v <= -1.0e29f ? 0.0f : __builtin_amdgcn_exp2f(v - mn);
+        sacc[kb][r] = e;
+        ps += e;
+      }
+    l = l * alpha + ps;
+#pragma unroll
+    for (int db = 0; db < 4; db++) oacc[db] *= alpha;
+
+    // ---- O^T += V^T P over four 16-key steps
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int kb = c >> 1, h2 = c & 1;
+      const f16x8 bp = {(f16)sacc[kb][8 * h2 + 0], (f16)sacc[kb][8 * h2 + 1], (f16)sacc[kb][8 * h2 + 2],
+                        (f16)sacc[kb][8 * h2 + 3], (f16)sacc[kb][8 * h2 + 4], (f16)sacc[kb][8 * h2 + 5],
+                        (f16)sacc[kb][8 * h2 + 6], (f16)sacc[kb][8 * h2 + 7]};
+      const uint32_t u1 = 8 * kb + 4 * h2 + gh, u2 = u1 + 2;   // 4-key units of the lane's 8 keys
+#pragma unroll
+      for (int db = 0; db < 4; db++) {
+        const uint32_t d = 32 * db + l32, sw = (d >> 1) & 15u;
+        const u32x2 lo = *(const u32x2 *)(sV[b] + d * AT_BK + ((u1 ^ sw) * 4));
+        const u32x2 hi = *(const u32x2 *)(sV[b] + d * AT_BK + ((u2 ^ sw) * 4));
+        const f16x8 av = __builtin_bit_cast(f16x8, (u32x4){lo.x, lo.y, hi.x, hi.y});
+        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bp, oacc[db], 0, 0, 0);
+      }
+    }
+    if (t + 1 < ntile) lstore(b ^ 1);
+    __syncthreads();
+  }
+
+  // ---- O = O^T / l: lane writes its query's 128 values in runs of 4 d
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  if (qw < p.Lq) {
+    uint16_t *orow = p.O + (size_t)qw * p.ldo + h * 128;
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; g4++) {
+        const uint32_t d = 32 * db + 8 * g4 + 4 * gh;
+        *(u32x2 *)(orow + d) = (u32x2){pack2(oacc[db][4 * g4] * inv, oacc[db][4 * g4 + 1] * inv),
+                                       pack2(oacc[db][4 * g4 + 2] * inv, oacc[db][4 * g4 + 3] * inv)};
+      }
+  }
+}
+
+hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
+  if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
+  dim3 grid((p.Lq + AT_BQ - 1) / AT_BQ, p.Hq);
+  hipLaunchKernelGGL(k_attention, grid, dim3(AT_NT), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace p0k

@@ -277,6 +277,35 @@ int prepare_rowstats(const p0k_rowstats_args *a, std::string *err) {
   return P0K_OK;
 }
 
+int prepare_attention(const p0k_attn_args *a, AttnParams *out, std::string *err) {
+  NEED(a != nullptr, "attention: no arguments");
+  NEED(a->struct_size == sizeof(p0k_attn_args), "attention: struct_size %u, this library expects %u", a->struct_size,
+       (unsigned)sizeof(p0k_attn_args));
+  NEED(a->q_buf && a->k_buf && a->v_buf && a->o_buf, "attention: missing q, k, v or o buffer");
+  const uint32_t Lq = a->Lq, Lk = a->Lk ? a->Lk : a->Lq, Hq = a->Hq, Hkv = a->Hkv ? a->Hkv : a->Hq;
+  const uint32_t nvalid = a->nvalid ? a->nvalid : Lk, ldo = a->ldo ? a->ldo : Hq * 128;
+  NEED(Lq > 0 && Lk > 0 && Hq > 0, "attention: Lq, Lk and Hq must be positive");
+  NEED(Hq % Hkv == 0, "attention: Hq %u is not a multiple of Hkv %u", Hq, Hkv);
+  NEED(a->mode <= 2, "attention: mode must be 0, 1 or 2");
+  NEED(nvalid <= Lk || a->mode == 0, "attention: nvalid %u exceeds Lk %u", nvalid, Lk);
+  NEED(a->q_off % 16 == 0 && a->k_off % 16 == 0 && a->v_off % 16 == 0, "attention: q / k / v offsets must be 16-byte aligned");
+  NEED(a->o_off % 8 == 0 && ldo % 4 == 0 && ldo >= Hq * 128, "attention: o offset 8-byte aligned, ldo a multiple of 4 covering Hq * 128");
+  FITS("q", a->q_off + (uint64_t)Hq * Lq * 256, a->q_size);
+  FITS("k", a->k_off + (uint64_t)Hkv * Lk * 256, a->k_size);
+  FITS("v", a->v_off + (uint64_t)Hkv * Lk * 256, a->v_size);
+  FITS("o", a->o_off + ((uint64_t)(Lq - 1) * ldo + Hq * 128) * 2, a->o_size);
+  if (out) {
+    out->Q = (const uint16_t *)((const uint8_t *)a->q_buf + a->q_off);
+    out->K = (const uint16_t *)((const uint8_t *)a->k_buf + a->k_off);
+    out->V = (const uint16_t *)((const uint8_t *)a->v_buf + a->v_off);
+    out->O = (uint16_t *)((uint8_t *)a->o_buf + a->o_off);
+    out->Lq = Lq; out->Lk = Lk; out->ldo = ldo; out->Hq = Hq; out->Hkv = Hkv; out->mode = a->mode; out->nvalid = nvalid;
+    out->scale = a->scale != 0.0f ? a->scale : 0.08838834764831845f;   // 1 / sqrt(128)
+    out->cap = a->cap;
+  }
+  return P0K_OK;
+}
+
 int prepare_pixstats(const p0k_pixstats_args *a, std::string *err) {
   NEED(a != nullptr, "pixstats: no arguments");
   NEED(a->struct_size == sizeof(p0k_pixstats_args), "pixstats: struct_size %u, this library expects %u", a->struct_size,

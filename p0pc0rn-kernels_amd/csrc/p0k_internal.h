@@ -13,6 +13,8 @@ struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; };
 int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err);
 int prepare_rowstats(const p0k_rowstats_args *a, std::string *err);
 int prepare_pixstats(const p0k_pixstats_args *a, std::string *err);
+struct AttnParams;
+int prepare_attention(const p0k_attn_args *a, AttnParams *out, std::string *err);
 // what: 1 = partial rows, 2 = finalize, 3 = both
 int prepare_gn(const p0k_gn_args *a, int what, std::string *err);
 }  // namespace p0k

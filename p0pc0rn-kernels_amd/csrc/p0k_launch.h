@@ -19,6 +19,14 @@ hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *c
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);
+// flash attention, head size 128 (src/ops/attention.js:168-201)
+struct AttnParams {
+  const uint16_t *Q, *K, *V;   // [Hq][Lq][128], [Hkv][Lk][128] f16
+  uint16_t *O;                 // [Lq][ldo] f16, head h at column h * 128
+  uint32_t Lq, Lk, ldo, Hq, Hkv, mode, nvalid;
+  float scale, cap;            // natural-log scale; cap > 0: scores -> cap * tanh(scores / cap)
+};
+hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 // pixstats and GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109)
 hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, float *r, hipStream_t s);
 hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);

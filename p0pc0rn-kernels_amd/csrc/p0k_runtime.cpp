@@ -393,6 +393,34 @@ int p0k_pixstats(p0k_ctx *c, const p0k_pixstats_args *a) {
   return P0K_OK;
 }
 
+int p0k_attention_check(const p0k_attn_args *a) {
+  std::string err;
+  int r = p0k::prepare_attention(a, nullptr, &err);
+  if (r) return set_err(r, err);
+  return P0K_OK;
+}
+
+double p0k_attention_flops(const p0k_attn_args *a) {
+  if (!a) return 0.0;
+  const double Lk = a->Lk ? a->Lk : a->Lq;
+  return 4.0 * a->Lq * Lk * 128.0 * a->Hq;
+}
+
+int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
+  if (!c) return set_err(P0K_E_ARG, "attention: NULL context");
+  std::string err;
+  p0k::AttnParams p;
+  int r = p0k::prepare_attention(a, &p, &err);
+  if (r) return set_err(r, err);
+  if ((r = check_live(c, a->q_buf, a->q_size, "attention", "q")) || (r = check_live(c, a->k_buf, a->k_size, "attention", "k")) ||
+      (r = check_live(c, a->v_buf, a->v_size, "attention", "v")) || (r = check_live(c, a->o_buf, a->o_size, "attention", "o")))
+    return r;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_attention(p, c->stream);
+  if (e != hipSuccess) return hip_err(e, "attention launch");
+  return P0K_OK;
+}
+
 uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
 
 static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {

@@ -4,6 +4,7 @@
 //   createGpu / Gpu (src/core/gpu.js:15, :30)      buffer, upload, read, free, done, poolStats, drainPool, freeAll, describe
 //   gemm(gpu, args) (src/ops/gemm.js:268)          same argument object, same synchronous argument errors, returns 2MNK
 //   rowstats(gpu, args) (src/ops/misc.js:37)       mean / rstd per row, the statistics the rms and lnmod prologues read
+//   attention(gpu, args) (src/ops/attention.js:168) head size 128, the consumer of the heads epilogue
 //   pixstats (src/ops/video.js:317), gnPartBytes / gnPartial / gnFinalize / groupnormStats (src/ops/misc.js:92-109)
 //   defaultTune / calibrate / tuneEntry / TUNE_TABLE (src/core/tune.js:18-58)
 //   loadWeights / uploadWeights (src/weights.js:10, :28)
@@ -242,6 +243,17 @@ function rowstats(gpu, a) {
   });
 }
 
+// ------------------------------------------------------------------ attention (src/ops/attention.js:168), head size 128
+/** attention(gpu, {q, k, v: {buf, off}, o: {buf, off, ld}, Lq, Lk, Hq, Hkv, mode, nvalid, scale, cap}) -> 4 Lq Lk 128 Hq */
+function attention(gpu, a) {
+  const t = (x) => ({ buf: ptrOf(x.buf), off: x.off || 0, size: x.size != null ? x.size + (x.off || 0) : sizeOf(x.buf) });
+  const q = t(a.q), k = t(a.k), v = t(a.v), o = t(a.o);
+  return call(addon().attention, gpu.ctx, { q_buf: q.buf, q_off: q.off, q_size: q.size, k_buf: k.buf, k_off: k.off,
+    k_size: k.size, v_buf: v.buf, v_off: v.off, v_size: v.size, o_buf: o.buf, o_off: o.off, o_size: o.size,
+    ldo: a.o.ld || 0, Lq: a.Lq, Lk: a.Lk || 0, Hq: a.Hq, Hkv: a.Hkv || 0, mode: a.mode || 0, nvalid: a.nvalid || 0,
+    scale: a.scale || 0, cap: a.cap || 0 });
+}
+
 // ------------------------------------------------------------------ conv prologue statistics (src/ops/video.js, misc.js)
 /** pixstats(gpu, {x: {buf, off}, r: {buf}, V, C, eps = 1e-8, ro}): r[ro + v] = 1 / sqrt(mean_c x[v][c]^2 + eps) */
 function pixstats(gpu, a) {
@@ -423,7 +435,7 @@ function encodedBytes(enc, rows, cols) {
 
 export {
   MB, GpuError, createGpu, Gpu, f2h, h2f, toF16, fromF16,
-  gemm, gemmPlan, gemmDesc, DEFAULT_TILE, rowstats, pixstats, gnPartBytes, gnPartial, gnFinalize, groupnormStats,
+  gemm, gemmPlan, gemmDesc, DEFAULT_TILE, rowstats, attention, pixstats, gnPartBytes, gnPartial, gnFinalize, groupnormStats,
   TUNE_TABLE, tuneEntry, defaultTune, calibrate,
   MANIFEST_FORMAT, loadWeights, uploadWeights,
   packQ4, packQ8, packF16, encodedBytes,

@@ -4,7 +4,7 @@
  * every argument check happens in libp0k, whose message becomes the thrown Error's message.
  *
  * Exports: ctxCreate, ctxDestroy, deviceInfo, alloc, free, upload, download, copy, sync, poolStats, drainPool,
- *          gemm, gemmCheck, selectTile, rowstats, pixstats, gn, gnPartBytes, packQ4, packQ8, packF16, tensorBytes,
+ *          gemm, gemmCheck, selectTile, rowstats, attention, pixstats, gn, gnPartBytes, packQ4, packQ8, packF16, tensorBytes,
  *          lastError, abiVersion
  * (N-API version 6 or later: BigInt support; Node 12.17+).
  */
@@ -425,6 +425,28 @@ static napi_value gn(napi_env env, napi_callback_info info) {   /* (ctx, desc, w
   return mk_num(env, nwg);
 }
 
+static napi_value attention(napi_env env, napi_callback_info info) {   /* (ctx, desc) -> flops */
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
+  napi_value o = argv[1];
+  p0k_attn_args a;
+  memset(&a, 0, sizeof a);
+  a.struct_size = sizeof a;
+  FIELD(o, "q_buf", a.q_buf, (const void *)(uintptr_t)); FIELD(o, "q_off", a.q_off, ); FIELD(o, "q_size", a.q_size, );
+  FIELD(o, "k_buf", a.k_buf, (const void *)(uintptr_t)); FIELD(o, "k_off", a.k_off, ); FIELD(o, "k_size", a.k_size, );
+  FIELD(o, "v_buf", a.v_buf, (const void *)(uintptr_t)); FIELD(o, "v_off", a.v_off, ); FIELD(o, "v_size", a.v_size, );
+  FIELD(o, "o_buf", a.o_buf, (void *)(uintptr_t)); FIELD(o, "o_off", a.o_off, ); FIELD(o, "o_size", a.o_size, );
+  FIELD(o, "ldo", a.ldo, ); FIELD(o, "Lq", a.Lq, ); FIELD(o, "Lk", a.Lk, ); FIELD(o, "Hq", a.Hq, ); FIELD(o, "Hkv", a.Hkv, );
+  FIELD(o, "mode", a.mode, ); FIELD(o, "nvalid", a.nvalid, );
+  if (!field_f32(env, o, "scale", &a.scale) || !field_f32(env, o, "cap", &a.cap)) {
+    napi_throw_type_error(env, NULL, "field scale / cap");
+    return NULL;
+  }
+  int r = p0k_attention(get_ctx(env, argv[0]), &a);
+  if (r) return throw_p0k(env, r);
+  return mk_num(env, p0k_attention_flops(&a));
+}
+
 static napi_value gnPartBytes(napi_env env, napi_callback_info info) {
   napi_value argv[1];
   if (!get_args(env, info, 1, argv)) return NULL;
@@ -513,7 +535,7 @@ static napi_value init(napi_env env, napi_value exports) {
       {"poolStats", poolStats}, {"drainPool", drainPool}, {"gemm", gemm}, {"gemmCheck", gemmCheck},
       {"selectTile", selectTile}, {"rowstats", rowstats}, {"packQ4", packQ4}, {"packQ8", packQ8},
       {"packF16", packF16}, {"tensorBytes", tensorBytes}, {"lastError", lastError}, {"abiVersion", abiVersion},
-      {"pixstats", pixstats}, {"gn", gn}, {"gnPartBytes", gnPartBytes},
+      {"pixstats", pixstats}, {"gn", gn}, {"gnPartBytes", gnPartBytes}, {"attention", attention},
   };
   for (size_t i = 0; i < sizeof fns / sizeof fns[0]; i++) {
     napi_value f;

@@ -85,6 +85,34 @@ class GnArgs(C.Structure):
     ]
 
 
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", C.c_uint32),
+        ("q_buf", C.c_void_p), ("q_off", C.c_uint64), ("q_size", C.c_uint64),
+        ("k_buf", C.c_void_p), ("k_off", C.c_uint64), ("k_size", C.c_uint64),
+        ("v_buf", C.c_void_p), ("v_off", C.c_uint64), ("v_size", C.c_uint64),
+        ("o_buf", C.c_void_p), ("o_off", C.c_uint64), ("o_size", C.c_uint64), ("ldo", C.c_uint32),
+        ("Lq", C.c_uint32), ("Lk", C.c_uint32), ("Hq", C.c_uint32), ("Hkv", C.c_uint32), ("mode", C.c_uint32),
+        ("nvalid", C.c_uint32), ("scale", C.c_float), ("cap", C.c_float),
+    ]
+
+
+def attn_args(a, resolve):
+    """attention(gpu, a) argument object (src/ops/attention.js:167) -> AttnArgs; resolve(buf) -> (pointer, size)."""
+    s = AttnArgs()
+    s.struct_size = C.sizeof(AttnArgs)
+    for key in ("q", "k", "v", "o"):
+        p, sz = resolve(a[key]["buf"])
+        setattr(s, key + "_buf", p)
+        setattr(s, key + "_off", _get(a[key], "off", 0))
+        setattr(s, key + "_size", sz)
+    s.ldo = _get(a["o"], "ld", 0)
+    s.Lq, s.Lk, s.Hq, s.Hkv = a["Lq"], _get(a, "Lk", 0), a["Hq"], _get(a, "Hkv", 0)
+    s.mode, s.nvalid = _get(a, "mode", 0), _get(a, "nvalid", 0)
+    s.scale, s.cap = _get(a, "scale", 0.0), _get(a, "cap", 0.0)
+    return s
+
+
 class Tile(C.Structure):
     _fields_ = [("bm", C.c_uint32), ("bn", C.c_uint32), ("kernel", C.c_int32)]
 
@@ -104,6 +132,7 @@ EXPORTS = [
     "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
+    "p0k_attention_check", "p0k_attention", "p0k_attention_flops",
     "p0k_pixstats", "p0k_gn_part_bytes", "p0k_gn_partial", "p0k_gn_finalize", "p0k_groupnorm_stats",
     "p0k_event_create", "p0k_event_record", "p0k_event_elapsed_ms", "p0k_event_destroy",
     "p0k_tensor_bytes", "p0k_pack_q4", "p0k_pack_q8", "p0k_pack_f16",
@@ -134,6 +163,8 @@ def lib():
             "p0k_select_tile": ([C.POINTER(GemmArgs), C.POINTER(Tile)], I),
             "p0k_rowstats_check": ([C.POINTER(RowstatsArgs)], I), "p0k_rowstats": ([P, C.POINTER(RowstatsArgs)], I),
             "p0k_pixstats": ([P, C.POINTER(PixstatsArgs)], I), "p0k_gn_part_bytes": ([C.c_uint32], U64),
+            "p0k_attention_check": ([C.POINTER(AttnArgs)], I), "p0k_attention": ([P, C.POINTER(AttnArgs)], I),
+            "p0k_attention_flops": ([C.POINTER(AttnArgs)], C.c_double),
             "p0k_gn_partial": ([P, C.POINTER(GnArgs), C.POINTER(C.c_uint32)], I),
             "p0k_gn_finalize": ([P, C.POINTER(GnArgs)], I), "p0k_groupnorm_stats": ([P, C.POINTER(GnArgs)], I),
             "p0k_event_create": ([P, C.POINTER(P)], I), "p0k_event_record": ([P, P], I),
@@ -325,6 +356,15 @@ class Device:
         r.mode, r.eps = (1 if mode == "rms" else 0), eps
         r.st_buf, r.st_off, r.st_size = st.ptr, st_off, st.size
         _chk(lib().p0k_rowstats(self.ctx, C.byref(r)))
+
+    def attention_raw(self, s):
+        _chk(lib().p0k_attention(self.ctx, C.byref(s)))
+
+    def attention(self, a):
+        """attention(gpu, a) of src/ops/attention.js:168 (head size 128); returns 4 Lq Lk 128 Hq."""
+        s = attn_args(a, self.resolve)
+        _chk(lib().p0k_attention(self.ctx, C.byref(s)))
+        return lib().p0k_attention_flops(C.byref(s))
 
     def pixstats(self, x, V, Cc, r, eps=0.0, ro=0, x_off=0):
         """pixstats(gpu, {x, r, V, C, eps, ro}) of src/ops/video.js:317."""

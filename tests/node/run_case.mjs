@@ -102,7 +102,11 @@ async function stats() {
   const part = g.buffer(p0k.gnPartBytes(spec.pix)), ab = g.buffer(spec.GC * 8);
   p0k.groupnormStats(g, { x: { buf: gx }, pix: spec.pix, C: spec.GC, part, gb: { buf: gb, gOff: 0, bOff: spec.GC * 4 }, ab: { buf: ab } });
   put('ab_gpu.f32', new Float32Array(await g.read(ab)));
-  [x, r, gx, gb, part, ab].forEach((b) => g.free(b));
+  const aq = g.upload(bin('aq.bin')), ak = g.upload(bin('ak.bin')), av = g.upload(bin('av.bin')), ao = g.buffer(spec.L * spec.H * 256);
+  const fl = p0k.attention(g, { q: { buf: aq }, k: { buf: ak }, v: { buf: av }, o: { buf: ao }, Lq: spec.L, Hq: spec.H, Hkv: 1, mode: 1, nvalid: spec.L });
+  put('ao_gpu.bin', new Uint8Array(await g.read(ao)));
+  writeFileSync(join(dir, 'result.json'), JSON.stringify({ attnFlops: fl }));
+  [x, r, gx, gb, part, ab, aq, ak, av, ao].forEach((b) => g.free(b));
   await g.done(); g.destroy();
 }
 

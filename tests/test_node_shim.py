@@ -152,8 +152,9 @@ def test_shim_load_weights(tmp_path):
 
 
 @pytest.mark.gpu
-def test_shim_pixstats_and_groupnorm(tmp_path):
-    """pixstats (src/ops/video.js:317) and groupnormStats (src/ops/misc.js:106) through the shim."""
+def test_shim_pixstats_groupnorm_attention(tmp_path):
+    """pixstats (src/ops/video.js:317), groupnormStats (src/ops/misc.js:106) and attention (src/ops/attention.js:168)
+    through the shim."""
     rng = np.random.default_rng(8)
     V, Cc, pix, GC = 500, 128, 300, 64
     x = oracle.f16_bits(rng.standard_normal(V * Cc).astype(np.float32))
@@ -162,8 +163,19 @@ def test_shim_pixstats_and_groupnorm(tmp_path):
     x.tofile(str(tmp_path / "x.bin"))
     gx.tofile(str(tmp_path / "gx.bin"))
     np.concatenate([g, b]).tofile(str(tmp_path / "gb.bin"))
-    (tmp_path / "spec.json").write_text(json.dumps({"V": V, "C": Cc, "pix": pix, "GC": GC}))
+    L, H = 70, 2
+    aq = oracle.f16_bits(oracle.randn(H * L * 128, 3, 0.5))
+    ak = oracle.f16_bits(oracle.randn(L * 128, 4, 0.5))
+    av = oracle.f16_bits(oracle.randn(L * 128, 5))
+    for n, a in (("aq", aq), ("ak", ak), ("av", av)):
+        a.tofile(str(tmp_path / f"{n}.bin"))
+    (tmp_path / "spec.json").write_text(json.dumps({"V": V, "C": Cc, "pix": pix, "GC": GC, "L": L, "H": H}))
     node("stats", tmp_path)
+    res = json.loads((tmp_path / "result.json").read_text())
+    assert res["attnFlops"] == 4 * L * L * 128 * H
+    ao = oracle.h2f(np.fromfile(str(tmp_path / "ao_gpu.bin"), np.uint16)[:L * H * 128])
+    aw = oracle.h2f(oracle.attention(aq, ak, av, L, L, H, 1, 1, L))
+    assert np.abs(ao - aw).max() <= 2 ** -8 * np.abs(aw).max() + 2 ** -9 * np.abs(aw).max()
     r = np.fromfile(str(tmp_path / "r_gpu.f32"), np.float32)[:V]
     np.testing.assert_allclose(r, oracle.pixstats(x, V, Cc, 1e-8), rtol=2e-6)
     ab = np.fromfile(str(tmp_path / "ab_gpu.f32"), np.float32)[:2 * GC]
