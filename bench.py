@@ -40,12 +40,12 @@ HBM_PEAK = 8.0e12          # B/s, MI355X published
 FP16_PEAK = 2.5e15         # FLOP/s dense fp16 MFMA, MI355X published
 MALL = 256 << 20
 
-# HBM bytes per launch from rocprofv3 counters (profiles/k_gemv_q4_swiglu_decode_M1.md): FETCH_SIZE and WRITE_SIZE in
+# HBM bytes per launch from rocprofv3 counters (profiles/k_gemv_q4_swiglu_decode_M1.md, k_gemv_mf_..._M16.md): FETCH_SIZE and WRITE_SIZE in
 # KiB per dispatch, each times what the same counter reads per byte of a plain 1 GiB device copy (`--copy-calib`:
 # FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run, so the
 # figures of the last profiled build are kept here, per workload.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36588, 28)}
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36588, 28), "decode_q4_swiglu_M16": (36900, 448)}
 
 
 def log(msg):
