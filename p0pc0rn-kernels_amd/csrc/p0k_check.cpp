@@ -243,8 +243,14 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   if (out) *out = p;
   if (plan) {
     plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128;
-    if (kernel == K_MFMA) {
-      mfma_tile(M, N, MI355X_CUS, &plan->bm, &plan->bn);
+    // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
+    if (kernel == K_MFMA && gemm_dma_ok(p, we, xm)) {
+      const char *ov = getenv("P0K_MFMA_KERNEL");
+      if (!ov || strcmp(ov, "reg") != 0) kernel = plan->kernel = K_MFMA_DMA;
+    }
+    if (kernel == K_MFMA_DMA) dma_tile(M, N, we, MI355X_CUS, &plan->bm, &plan->bn);
+    if (kernel == K_MFMA) mfma_tile(M, N, MI355X_CUS, &plan->bm, &plan->bn);
+    if (kernel == K_MFMA || kernel == K_MFMA_DMA) {
       // tuning / test override of the tile (P0K_MFMA_TILE=256x128); results do not depend on it
       if (const char *ov = getenv("P0K_MFMA_TILE")) {
         unsigned tm = 0, tn = 0;

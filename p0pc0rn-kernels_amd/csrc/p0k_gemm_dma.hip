@@ -1,0 +1,458 @@
+// p0k_gemm_dma.hip — the prefill path of `gemm` (src/ops/gemm.js:29-257) for row-major fp16 activations: operands
+// move global -> LDS by the load-to-LDS path (global_load_lds_dwordx4 / _dword: each lane's bytes land at
+// M0 + 16 lane / 4 lane, no registers, no LDS store instructions), weights are decoded in registers right before the
+// matrix core uses them.
+//
+// One workgroup (4 waves, 2 x 2) computes a TBM x TBN tile (TBM, TBN in {128, 256}); a wave owns (TBM/2) x (TBN/2)
+// as 32x32 v_mfma_f32_32x32x16_f16 blocks. K moves in steps of 64 through a ring of S LDS stages:
+//   X' rows      [row][128 B], the 16-byte chunk c of row r at c ^ ((r >> 1) & 7)
+//   f16 weights  the same layout, one row per ws column
+//   q4 records   per 64-column block and 32-k record: the 64 code rows [col][16 B] as stored, and the 64 (scale, min)
+//                words [col][4 B]; q8 records: the code rows as four 16-byte chunks [chunk][col][16 B] and the scale
+//                words [col][4 B] (the word holding the row's fp16 scale)
+// Column `col` of the tile reads weight row wrow(col) (GLU interleave and clamping in wrow), so one DMA instruction
+// gathers 64 columns' records in place. A step is four 16-k sub-steps; lane l takes A row l % 32 and B column l % 32
+// of its blocks and k = 32 h + 8 s .. + 7 (h = l / 32, s = sub-step): the 8 codes of ONE q4 code word (word s of
+// record h), half of one q8 16-byte chunk, one f16 chunk. Decoding follows p0k_device.h bit for bit in value (the q4
+// odd nibble is read in place as the fp16 1024 + 16 q and scaled by s / 16, exact because s / 16 is a normal fp16
+// whenever the fast path is taken), in natural k order, so X' needs no permutation.
+//
+// Pipeline (per wave): the sub-step's MFMAs are interleaved with the LDS reads of the next sub-step's X' fragments,
+// the decode of its weight fragments and one third of the DMA refill of the stage freed at the last barrier. One
+// barrier per step: before it, s_waitcnt vmcnt(n) leaves only the refills younger than the next stage in flight; the
+// DMA instructions are invisible to the compiler (inline asm), so every wait on them is explicit and exact.
+// After the last step the fp32 accumulators go through LDS in 128 x 128 quadrants to the shared epilogue. The K
+// order of every output element is fixed (no split-K) and independent of the tile.
+#include "p0k_device.h"
+#include "p0k_launch.h"
+
+namespace p0k {
+
+namespace {
+
+constexpr int DBK = 64, DNT = 256, DLDC = 128 + 4;
+
+template <int WE, int TBM, int TBN>
+struct DT {
+  static constexpr int NBLK = TBN / 64;                                        // 64-column weight blocks
+  static constexpr int A_BYTES = TBM * 128;
+  static constexpr int BC_BYTES = WE == W_F16 ? TBN * 128 : (WE == W_Q4 ? NBLK * 2 * 1024 : NBLK * 4 * 1024);
+  static constexpr int BS_BYTES = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 * 256 : 4 * 256);   // q8: NBLK or pad
+  static constexpr int STAGE = A_BYTES + BC_BYTES + BS_BYTES;
+  static constexpr bool TWO = 4 * STAGE <= 160 * 1024 && TBM * TBN < 256 * 256;  // two workgroups per CU
+  static constexpr int BUDGET = TWO ? 80 * 1024 : 160 * 1024;
+  static constexpr int S = 3 * STAGE <= BUDGET ? 3 : 2;
+  static constexpr int SMEM_C = 128 * DLDC * 4;
+  static constexpr int SMEM = S * STAGE > SMEM_C ? S * STAGE : SMEM_C;
+  static_assert(SMEM <= BUDGET, "LDS budget");
+  // DMA instructions per stage, in groups of four (one per wave): X' row blocks (8 rows), weight code blocks, then
+  // weight scale words (q8: padded to 4 with repeats of the last block's)
+  static constexpr int NIA = TBM / 8;
+  static constexpr int NIC = WE == W_F16 ? TBN / 8 : (WE == W_Q4 ? NBLK * 2 : NBLK * 4);
+  static constexpr int NIS = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 : 4);
+  static constexpr int NW = (NIA + NIC + NIS) / 4;                             // per wave
+  static constexpr int WA = NIA / 4, WC = NIC / 4;
+  static constexpr int BI = TBM / 64, BJ = TBN / 64;                           // 32x32 blocks per wave
+  static constexpr int OCC = TWO ? 2 : 1;
+};
+
+__device__ __forceinline__ uint32_t lds_u32(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// load-to-LDS of 16 (4) bytes per lane: lane l writes LDS [m0 + 16 l] ([m0 + 4 l])
+__device__ __forceinline__ void dma16(const void *src, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(src) : "memory");
+}
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14])
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// q4: the (scale, min) word allows the fast decode (p0k_device.h) and s / 16 is exact
+__device__ __forceinline__ bool q4n_fast_ok(uint32_t sm) {
+  const uint32_t es = (sm >> 10) & 31u;
+  return q4_fast_ok(sm) && (es >= 5u || (sm & 0x7fffu) == 0u);
+}
+// q4 code word (k0..k7, low nibble first) -> f16x8 in natural order
+__device__ __forceinline__ f16x8 dq4_fast(uint32_t w, f16x2 s2, f16x2 m2) {
+  const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    // byte i to bytes 0 and 2: (q_2i | 16 q_2i+1) in both halves; the mask keeps q_2i low, 16 q_2i+1 high
+    const uint32_t t = perm(w, w, 0x0c000c00u | (uint32_t)i | ((uint32_t)i << 16));
+    const uint32_t v = (t & 0x00F0000Fu) | 0x64006400u;
+    o[i] = as_u(__builtin_elementwise_fma(as_h2(v) - k1024, s2, m2));
+  }
+  return __builtin_bit_cast(f16x8, (u32x4){o[0], o[1], o[2], o[3]});
+}
+__device__ __forceinline__ f16x8 dq4_slow(uint32_t w, uint32_t sm) {
+  const f16x2 sm2 = as_h2(sm);
+  const float s = (float)sm2.x, mn = (float)sm2.y;
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float a = fmaf((float)((w >> (8 * i)) & 15u), s, mn), b = fmaf((float)((w >> (8 * i + 4)) & 15u), s, mn);
+    asm volatile("" : "+v"(a), "+v"(b));   // fp32 rounding first, as the reference (no fused fma + cvt)
+    o[i] = as_u((f16x2){(f16)a, (f16)b});
+  }
+  return __builtin_bit_cast(f16x8, (u32x4){o[0], o[1], o[2], o[3]});
+}
+// q8: two code words (k0..k7 as signed bytes) -> f16x8 natural order, f16(q * s)
+__device__ __forceinline__ f16x8 dq8(uint32_t w0, uint32_t w1, f16x2 s2) {
+  const f16x2 k1152 = {(f16)1152.0f, (f16)1152.0f};
+  const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+  const uint32_t o0 = as_u((as_h2(perm(0x64646464u, u0, 0x04010400u)) - k1152) * s2);
+  const uint32_t o1 = as_u((as_h2(perm(0x64646464u, u0, 0x04030402u)) - k1152) * s2);
+  const uint32_t o2 = as_u((as_h2(perm(0x64646464u, u1, 0x04010400u)) - k1152) * s2);
+  const uint32_t o3 = as_u((as_h2(perm(0x64646464u, u1, 0x04030402u)) - k1152) * s2);
+  return __builtin_bit_cast(f16x8, (u32x4){o0, o1, o2, o3});
+}
+
+__device__ __forceinline__ void tile_order(const Params &p, uint32_t bid, uint32_t &mt, uint32_t &nt) {
+  // consecutive workgroups go to different XCDs: regroup per XCD, then walk bands of 8 M-tiles (shared L2 rows)
+  const uint32_t total = p.tilesM * p.tilesN;
+  uint32_t t = bid;
+  if ((total & 7u) == 0u) t = (bid & 7u) * (total >> 3) + (bid >> 3);
+  const uint32_t band = 8u, per = band * p.tilesN, g = t / per, first = g * band;
+  const uint32_t rows = p.tilesM - first < band ? p.tilesM - first : band, in = t - g * per;
+  mt = first + in % rows;
+  nt = in / rows;
+}
+
+template <int WE, int TBM, int TBN>
+__global__ __launch_bounds__(DNT, (DT<WE, TBM, TBN>::OCC))
+__attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::OCC)))) void k_gemm_dma(Params p) {
+  using T = DT<WE, TBM, TBN>;
+  constexpr int S = T::S, BI = T::BI, BJ = T::BJ, NW = T::NW;
+  constexpr int WTM = TBM / 2, WTN = TBN / 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[T::SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t mt, nt;
+  tile_order(p, blockIdx.x, mt, nt);
+  const uint32_t mB = mt * TBM, nB = nt * TBN;
+  const uint32_t nk = p.K / DBK;
+
+  // ---- per-lane DMA sources (step 0) and per-step advances; instruction t of this wave is number 4 t + wave of
+  //      the stage's list
+  const uint8_t *src[NW];
+  uint32_t dst[NW];                                   // byte offset inside a stage
+#pragma unroll
+  for (int t = 0; t < NW; t++) {
+    const int q = 4 * t + wave;
+    if (t < T::WA) {                                  // X' rows 8q .. 8q+7
+      const uint32_t r = 8 * q + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
+      uint32_t m = mB + r;
+      m = m < p.M ? m : p.M - 1u;
+      src[t] = p.X + ((size_t)m * p.ldx + p.kx0 + 8 * c) * 2;
+      dst[t] = q * 1024;
+    } else if (t < T::WA + T::WC) {
+      const int b = q - 4 * T::WA;
+      if constexpr (WE == W_F16) {                    // weight rows of ws columns 8b .. 8b+7
+        const uint32_t r = 8 * b + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
+        src[t] = p.W + ((size_t)wrow(p, nB + r) * p.wG + p.wk0 + 8 * c) * 2;
+      } else if constexpr (WE == W_Q4) {              // block b / 2, record b & 1: code row of column lane
+        const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
+        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + (r & 63u) * 16u;
+      } else {                                        // block b / 4, chunk b & 3
+        const uint32_t r = wrow(p, nB + 64 * (b >> 2) + lane);
+        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + (r & 63u) * 64u + (b & 3) * 16u;
+      }
+      dst[t] = T::A_BYTES + b * 1024;
+    } else {
+      const int b = q - 4 * (T::WA + T::WC);
+      if constexpr (WE == W_Q4) {                     // (scale, min) word of block b / 2, record b & 1
+        const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
+        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + 1024u + (r & 63u) * 4u;
+      } else if constexpr (WE == W_Q8) {              // scale pair word of block b (repeats past the last block)
+        const int bb = b < T::NBLK ? b : T::NBLK - 1;
+        const uint32_t r = wrow(p, nB + 64 * bb + lane);
+        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + 4096u + (r & 62u) * 2u;
+      }
+      dst[t] = T::A_BYTES + T::BC_BYTES + b * 256;
+    }
+  }
+  constexpr uint32_t WSTEP = WE == W_F16 ? 128u : (WE == W_Q4 ? 2560u : 4224u);
+  const uint32_t smem0 = lds_u32(smem);
+  // issue part `part` (instructions part*NP ..) of step kt into stage st
+  constexpr int NP = (NW + 2) / 3;
+  auto issue = [&](uint32_t kt, int st, int part) __attribute__((always_inline)) {
+    kt = kt < nk ? kt : nk - 1u;
+#pragma unroll
+    for (int t = part * NP; t < (part + 1) * NP && t < NW; t++) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(smem0 + st * T::STAGE + dst[t]);
+      if (t < T::WA) dma16(src[t] + (size_t)kt * 128u, m0);
+      else if (t < T::WA + T::WC) dma16(src[t] + (size_t)kt * WSTEP, m0);
+      else dma4(src[t] + (size_t)kt * WSTEP, m0);
+    }
+  };
+
+  // ---- fragments
+  const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, hh = lane >> 5, sw = (l32 >> 1) & 7;
+  const int rdA = (wm * WTM + l32) * 128;              // byte offset of the lane's first A row in a stage
+  f32x16 acc[BI][BJ];
+#pragma unroll
+  for (int i = 0; i < BI; i++)
+#pragma unroll
+    for (int j = 0; j < BJ; j++) acc[i][j] = (f32x16){};
+  f16x8 FA[2][BI], FB[2][BJ];
+  // weight words of the current step: q4 code row (4 words = 4 sub-steps) + (scale, min); q8 two chunks + scale word
+  u32x4 bc[BJ][WE == W_Q8 ? 2 : 1];
+  uint32_t bs[BJ];
+  uint32_t rodd = 0;                                   // q8: bit j = the column's weight row is odd (scale high half)
+  if constexpr (WE == W_Q8) {
+#pragma unroll
+    for (int j = 0; j < BJ; j++) rodd |= (wrow(p, nB + wn * WTN + 32 * j + l32) & 1u) << j;
+  }
+  auto rdA_frag = [&](f16x8 *F, int st, int sub) __attribute__((always_inline)) {
+    const uint8_t *sp = smem + st * T::STAGE + rdA + (((4 * hh + sub) ^ sw) & 7) * 16;
+#pragma unroll
+    for (int i = 0; i < BI; i++) F[i] = *(const f16x8 *)(sp + i * 32 * 128);
+  };
+  auto rdB_f16 = [&](f16x8 *F, int st, int sub) __attribute__((always_inline)) {
+    const uint8_t *sp = smem + st * T::STAGE + T::A_BYTES + (wn * WTN + l32) * 128 + (((4 * hh + sub) ^ sw) & 7) * 16;
+#pragma unroll
+    for (int j = 0; j < BJ; j++) F[j] = *(const f16x8 *)(sp + j * 32 * 128);
+  };
+  auto rdB_codes = [&](int st) __attribute__((always_inline)) {
+    const uint8_t *sb = smem + st * T::STAGE + T::A_BYTES;
+#pragma unroll
+    for (int j = 0; j < BJ; j++) {
+      const int col = wn * WTN + 32 * j + l32, blk = col >> 6, cb = col & 63;
+      if constexpr (WE == W_Q4) {
+        bc[j][0] = *(const u32x4 *)(sb + (blk * 2 + hh) * 1024 + cb * 16);
+        bs[j] = *(const uint32_t *)(sb + T::BC_BYTES + (blk * 2 + hh) * 256 + cb * 4);
+      } else if constexpr (WE == W_Q8) {
+        bc[j][0] = *(const u32x4 *)(sb + (blk * 4 + 2 * hh) * 1024 + cb * 16);
+        bc[j][1] = *(const u32x4 *)(sb + (blk * 4 + 2 * hh + 1) * 1024 + cb * 16);
+        bs[j] = *(const uint32_t *)(sb + T::BC_BYTES + blk * 256 + cb * 4);
+      }
+    }
+  };
+  // decode the weight fragments of sub-step `sub` from bc / bs
+  auto decode = [&](f16x8 *F, int sub) __attribute__((always_inline)) {
+    if constexpr (WE == W_Q4) {
+      bool fast = true;
+#pragma unroll
+      for (int j = 0; j < BJ; j++) fast = fast && q4n_fast_ok(bs[j]);
+      if (__builtin_expect(__all(fast), 1)) {
+#pragma unroll
+        for (int j = 0; j < BJ; j++) {
+          const f16x2 sm2 = as_h2(bs[j]);
+          const f16x2 s2 = {sm2.x, sm2.x * (f16)0.0625f}, m2 = {sm2.y, sm2.y};
+          F[j] = dq4_fast(bc[j][0][sub], s2, m2);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < BJ; j++) {
+          if (q4n_fast_ok(bs[j])) {
+            const f16x2 sm2 = as_h2(bs[j]);
+            const f16x2 s2 = {sm2.x, sm2.x * (f16)0.0625f}, m2 = {sm2.y, sm2.y};
+            F[j] = dq4_fast(bc[j][0][sub], s2, m2);
+          } else {
+            F[j] = dq4_slow(bc[j][0][sub], bs[j]);
+          }
+        }
+      }
+    } else if constexpr (WE == W_Q8) {
+#pragma unroll
+      for (int j = 0; j < BJ; j++) {
+        const uint32_t sh = ((rodd >> j) & 1u) ? (bs[j] >> 16) : (bs[j] & 0xffffu);
+        const f16x2 s2 = as_h2(sh | (sh << 16));
+        const u32x4 &c = bc[j][sub >> 1];
+        F[j] = (sub & 1) ? dq8(c.z, c.w, s2) : dq8(c.x, c.y, s2);
+      }
+    }
+  };
+  auto mfma = [&](const f16x8 *A, const f16x8 *B) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < BJ; j++)
+#pragma unroll
+      for (int i = 0; i < BI; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[j], acc[i][j], 0, 0, 0);
+  };
+  // interleave a sub-step: MFMA, then a share of the VALU decode, then an LDS read
+  auto sched = [&]() __attribute__((always_inline)) {
+    constexpr int NMF = BI * BJ, NRD = BI + (WE == W_F16 ? BJ : 0);
+    constexpr int NV = WE == W_F16 ? 0 : (WE == W_Q4 ? 18 * BJ : 16 * BJ);
+    constexpr int VPM = (NV + NMF - 1) / NMF;
+#pragma unroll
+    for (int q = 0; q < NMF; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (VPM) __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+      if (q < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  // ---- prologue: stages 0 .. S-2 in full; the refill of stage S-1 goes out during step 0
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+#pragma unroll
+    for (int part = 0; part < 3; part++) issue(s, s, part);
+  wait_vm<(S - 2) * NW>();
+  stage_barrier();
+  rdA_frag(FA[0], 0, 0);
+  if constexpr (WE == W_F16) {
+    rdB_f16(FB[0], 0, 0);
+  } else {
+    rdB_codes(0);
+    decode(FB[0], 0);
+  }
+  int st = 0, pst = S - 1;
+  uint32_t pk = S - 1;
+  for (uint32_t kt = 0; kt < nk; kt++) {
+#pragma unroll
+    for (int sub = 0; sub < 3; sub++) {
+      f16x8 *An = FA[(sub + 1) & 1], *Bn = FB[(sub + 1) & 1];
+      rdA_frag(An, st, sub + 1);
+      if constexpr (WE == W_F16) rdB_f16(Bn, st, sub + 1);
+      issue(pk, pst, sub);
+      if constexpr (WE != W_F16) decode(Bn, sub + 1);
+      mfma(FA[sub & 1], FB[sub & 1]);
+      sched();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the next stage has landed (own loads: only the refills of later stages may stay in flight), every wave is done
+    // with this one (its fragments are in registers), then refill it with step kt + S
+    const int sn = st + 1 == S ? 0 : st + 1;
+    wait_vm<(S - 2) * NW>();
+    wait_lgkm0();
+    stage_barrier();
+    pk = kt + S;
+    pst = st;
+    rdA_frag(FA[0], sn, 0);
+    if constexpr (WE == W_F16) {
+      rdB_f16(FB[0], sn, 0);
+      mfma(FA[1], FB[1]);
+    } else {
+      // the last sub-step's weight fragments are decoded: the codes of the next step may replace them
+      rdB_codes(sn);
+      mfma(FA[1], FB[1]);
+      decode(FB[0], 0);
+    }
+    sched();
+    __builtin_amdgcn_sched_barrier(0);
+    st = sn;
+  }
+  wait_vm<0>();
+  wait_lgkm0();
+  stage_barrier();
+
+  // ---- accumulators -> LDS one 128 x 128 quadrant at a time (32x32 layout: lane l, register r -> row
+  //      8 (r / 4) + 4 (l / 32) + r % 4, column l % 32), then the epilogue
+  float *sC = (float *)smem;
+#pragma unroll
+  for (int v = 0; v < TBM / 128; v++)
+#pragma unroll
+    for (int h = 0; h < TBN / 128; h++) {
+      const int r0 = wm * WTM - v * 128, c0 = wn * WTN - h * 128;
+      if (r0 >= 0 && r0 < 128 && c0 >= 0 && c0 < 128) {
+#pragma unroll
+        for (int i = 0; i < BI; i++)
+#pragma unroll
+          for (int j = 0; j < BJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const int row = r0 + i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+              sC[row * DLDC + c0 + j * 32 + l32] = acc[i][j][r];
+            }
+      }
+      __syncthreads();
+      epilogue<DNT>(p, sC, DLDC, 128, mB + v * 128, nB + h * 128, tid);
+      if (v + 1 < TBM / 128 || h + 1 < TBN / 128) __syncthreads();
+    }
+}
+
+template <int WE, int TBM, int TBN>
+hipError_t launch_dma_one(const Params &p, hipStream_t s) {
+  Params q = p;
+  q.tilesM = (p.M + TBM - 1) / TBM;
+  q.tilesN = (p.N + TBN - 1) / TBN;
+  hipLaunchKernelGGL((k_gemm_dma<WE, TBM, TBN>), dim3(q.tilesM * q.tilesN), dim3(DNT), 0, s, q);
+  return hipGetLastError();
+}
+
+template <int WE>
+hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
+  if (bm == 256 && bn == 256) return launch_dma_one<WE, 256, 256>(p, s);
+  if (bm == 256 && bn == 128) return launch_dma_one<WE, 256, 128>(p, s);
+  if (bm == 128 && bn == 256) return launch_dma_one<WE, 128, 256>(p, s);
+  if (bm == 128 && bn == 128) return launch_dma_one<WE, 128, 128>(p, s);
+  return hipErrorInvalidValue;
+}
+
+// X' of the rms / lnmod prologues, materialised once: Xp[m][k] = xload8 (the fused prologue's exact values)
+template <int XM>
+__global__ __launch_bounds__(256) void k_xprep(Params p, uint16_t *xp) {
+  const uint32_t k8 = p.K / 8;
+  const uint64_t n = (uint64_t)p.M * k8;
+  for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < n; t += (uint64_t)gridDim.x * 256) {
+    const uint32_t m = (uint32_t)(t / k8), kq = (uint32_t)(t - (uint64_t)m * k8);
+    *(u32x4 *)(xp + (size_t)m * p.K + 8 * kq) = xload8<XM, 1>(p, m, RowCtx{0, 0, 0}, 8 * kq);
+  }
+}
+
+}  // namespace
+
+bool gemm_dma_ok(const Params &p, int we, int xm) {
+  if (xm != X_F16 && xm != X_RMS && xm != X_LNMOD) return false;
+  if (p.K % DBK != 0 || p.K == 0) return false;
+  if (xm == X_F16 && !(p.flags & F_XALIGN8)) return false;
+  if (we == W_F16 && !(p.flags & F_WALIGN8)) return false;
+  if (we == W_Q4 && p.wk0 % 32 != 0) return false;
+  if (we == W_Q8 && p.wk0 % 64 != 0) return false;
+  return we == W_F16 || we == W_Q4 || we == W_Q8;
+}
+
+hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
+  const uint64_t n = (uint64_t)p.M * (p.K / 8);
+  const unsigned blocks = (unsigned)(n / 256 < 4096 ? (n + 255) / 256 : 4096);
+  if (xm == X_RMS) hipLaunchKernelGGL(k_xprep<X_RMS>, dim3(blocks), dim3(256), 0, s, p, xp);
+  else if (xm == X_LNMOD) hipLaunchKernelGGL(k_xprep<X_LNMOD>, dim3(blocks), dim3(256), 0, s, p, xp);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// The tile: each candidate scored by its relative per-CU rate times the fraction of workgroup slots (one or two per
+// CU, as the tile's LDS allows) that hold real work over the rounds the grid needs.
+void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsigned *bn) {
+  auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
+    if (m == 256 && n == 256) return 1;
+    if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::OCC) : (DT<W_F16, 128, 256>::OCC);
+    if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::OCC : (m == 128 ? DT<W_Q4, 128, 256>::OCC : DT<W_Q4, 256, 128>::OCC);
+    return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::OCC : (m == 128 ? DT<W_Q8, 128, 256>::OCC : DT<W_Q8, 256, 128>::OCC);
+  };
+  struct C { unsigned m, n; double rate; } cand[] = {{256, 256, 1.0}, {128, 256, 0.85}, {256, 128, 0.85}, {128, 128, 0.7}};
+  double best = -1.0;
+  for (const C &c : cand) {
+    if (c.n == 256 && N <= 128) continue;
+    if (c.m == 256 && M <= 128) continue;
+    const uint64_t tiles = (uint64_t)((M + c.m - 1) / c.m) * ((N + c.n - 1) / c.n), slots = (uint64_t)cus * per_cu(c.m, c.n);
+    const double rounds = (double)((tiles + slots - 1) / slots);
+    const double useful = (double)M * N / ((double)c.m * c.n * rounds * slots);
+    const double score = c.rate * useful;
+    if (score > best + 1e-9) { best = score; *bm = c.m; *bn = c.n; }
+  }
+}
+
+hipError_t launch_gemm_dma(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s) {
+  switch (we) {
+  case W_Q4: return launch_dma_we<W_Q4>(p, bm, bn, s);
+  case W_Q8: return launch_dma_we<W_Q8>(p, bm, bn, s);
+  case W_F16: return launch_dma_we<W_F16>(p, bm, bn, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace p0k

@@ -6,7 +6,7 @@
 
 namespace p0k {
 struct Params;
-enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2 };
+enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2, K_MFMA_DMA = 3 };
 // kernel choice of one call: GEMV items are (128-column tile) x (K slice of KS), S slices per tile
 struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; };
 // validate a gemm call and translate it to kernel parameters (device pointers are filled in by the caller)

@@ -56,6 +56,9 @@ struct p0k_ctx {
   uint64_t ws_part_bytes = 0;
   uint32_t *ws_cnt = nullptr;
   static constexpr uint32_t WS_COUNTERS = 1u << 16;
+  // X' of the rms / lnmod prologues for the load-to-LDS GEMM (M x K fp16, grown on demand)
+  void *ws_x = nullptr;
+  uint64_t ws_x_bytes = 0;
 };
 
 struct p0k_event { hipEvent_t ev; int device; };
@@ -95,6 +98,7 @@ void p0k_ctx_destroy(p0k_ctx *c) {
   for (auto &kv : c->pool)
     for (auto &b : kv.second) (void)hipFree(b.ptr);
   if (c->ws_part) (void)hipFree(c->ws_part);
+  if (c->ws_x) (void)hipFree(c->ws_x);
   if (c->ws_cnt) (void)hipFree(c->ws_cnt);
   (void)hipStreamDestroy(c->stream);
   delete c;
@@ -292,6 +296,25 @@ static int check_operand(p0k_ctx *c, const void *buf, uint64_t size, const char 
   return P0K_OK;
 }
 
+// grow a workspace of the context to `need` bytes (not while the stream is being captured into a graph)
+static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t need, const char *what) {
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (need <= *bytes) return P0K_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return set_err(P0K_E_ARG, std::string("gemm: the ") + what + " workspace must grow (" + std::to_string(need) +
+                                  " bytes): make one call of this shape before capturing a graph");
+  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  if (*buf) HIPCHK(hipFree(*buf), "hipFree");
+  *buf = nullptr;
+  *bytes = 0;
+  hipError_t me = hipMalloc(buf, need);
+  if (me != hipSuccess) return set_err(P0K_E_NOMEM, std::string("gemm: ") + what + " workspace of " + std::to_string(need) + " bytes");
+  *bytes = need;
+  return P0K_OK;
+}
+
 int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   if (!c) return set_err(P0K_E_ARG, "gemm: NULL context");
   std::string err;
@@ -321,23 +344,21 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
     if (plan.S > 1) {
       if (tiles > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "gemm: N too large for the decode workspace");
       const uint64_t need = (uint64_t)plan.S * a->M * tiles * 128u * sizeof(float);
-      std::lock_guard<std::mutex> lk(c->mu);
-      if (need > c->ws_part_bytes) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        HIPCHK(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
-        if (cs != hipStreamCaptureStatusNone)
-          return set_err(P0K_E_ARG, "gemm: the decode workspace must grow (" + std::to_string(need) +
-                                        " bytes): make one call of this shape before capturing a graph");
-        HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        if (c->ws_part) HIPCHK(hipFree(c->ws_part), "hipFree");
-        c->ws_part = nullptr;
-        c->ws_part_bytes = 0;
-        hipError_t me = hipMalloc((void **)&c->ws_part, need);
-        if (me != hipSuccess) return set_err(P0K_E_NOMEM, "gemm: workspace of " + std::to_string(need) + " bytes");
-        c->ws_part_bytes = need;
-      }
+      if (int rr = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "decode")) return rr;
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF);
+  } else if (plan.kernel == p0k::K_MFMA_DMA) {
+    if (plan.xm != P0K_X_F16) {
+      // the prologue once per element into the X' workspace; the GEMM then reads fp16 rows
+      const uint64_t need = (uint64_t)a->M * a->K * 2u;
+      if (int rr = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return rr;
+      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)c->ws_x, c->stream);
+      if (e != hipSuccess) return hip_err(e, "gemm prologue launch");
+      p.X = (const uint8_t *)c->ws_x;
+      p.ldx = a->K;
+      p.kx0 = 0;
+    }
+    e = p0k::launch_gemm_dma(p, plan.we, plan.bm, plan.bn, c->stream);
   } else {
     e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, plan.bm, plan.bn, c->stream);
   }

@@ -469,4 +469,4 @@ def select_tile(a):
     s = gemm_args(a, lambda b: (b.ptr, b.size) if isinstance(b, Buffer) else numpy_resolve(b))
     t = Tile()
     _chk(lib().p0k_select_tile(C.byref(s), C.byref(t)))
-    return {"BM": t.bm, "BN": t.bn, "kernel": {1: "gemv", 2: "gemv_mfma"}.get(t.kernel, "mfma")}
+    return {"BM": t.bm, "BN": t.bn, "kernel": {1: "gemv", 2: "gemv_mfma", 3: "mfma_dma"}.get(t.kernel, "mfma")}

@@ -131,7 +131,8 @@ def test_kernel_choice():
     assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv"
     assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv_mfma"
-    assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma"
+    assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma_dma"          # fp16 rows, K % 64 == 0
+    assert p0k.select_tile(host_args(make_case(M=17, K=96)))["kernel"] == "mfma"         # K % 64 != 0
     c = make_conv3_case(T=1, H=2, W=2)                     # M = 4, a convolution: always the MFMA kernel
     assert p0k.select_tile(host_args(c))["kernel"] == "mfma"
     assert p0k.lib().p0k_gemm_flops(C.byref(p0k.gemm_args(host_args(make_case(M=3, N=64, K=32)), p0k.numpy_resolve))) == 2 * 3 * 64 * 32

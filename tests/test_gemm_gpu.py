@@ -80,16 +80,23 @@ EPIS = [
 @pytest.mark.parametrize("M", [1, 2, 4, 16, 70])
 @pytest.mark.parametrize("enc", ["f16", "q4g32a.t64", "q8g64s.t64"])
 @pytest.mark.parametrize("xmode,epi,kw", EPIS, ids=[f"{x}-{e}-{i}" for i, (x, e, _) in enumerate(EPIS)])
-def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw):
+def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     kw = dict(kw)
     N = {"heads": (kw.get("Hq", 1) + 2 * kw.get("Hkv", 1)) * 128, "swiglu": 384, "onormgate": 256}.get(epi, 192)
     K = 256
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if M == 1 else "gemv_mfma" if M <= 16 else "mfma")
+    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    assert kern == ("gemv" if M == 1 else "gemv_mfma" if M <= 16 else "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
+    if kern == "mfma_dma":
+        # the register-staged MFMA kernel on the same call
+        monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
+        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma"
+        got = c.run_device(dev)
+        assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M} register-staged")
 
 
 # ------------------------------------------------------------------------------------------------ dequantisation
@@ -253,23 +260,31 @@ TILE_CASES = [
     dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=260, N=512, K=128, Hq=2, Hkv=1, Ltot=300, row_off=7),
     dict(enc="f16", xmode="lnmod", epi="bias", M=140, N=384, K=192, res=True),
     dict(enc="q4g32a.t64", epi="onormgate", M=129, N=256, K=64),
+    dict(enc="q4g32a.t64", epi="f16", M=200, N=320, K=192, ld_pad=8, k0=64, wk0=32),
+    dict(enc="q8g64s.t64", epi="f32", M=333, N=192, K=128, ld_pad=16, k0=8, wk0=64),
 ]
 
 
+@pytest.mark.parametrize("kernel", ["mfma_dma", "mfma"])
 @pytest.mark.parametrize("kw", TILE_CASES, ids=lambda k: f"{k['enc']}-{k.get('xmode', 'f16')}-{k['epi']}")
-def test_every_mfma_tile_matches_oracle(dev, kw, monkeypatch):
-    """Each workgroup tile the library can choose (P0K_MFMA_TILE forces one) gives the oracle's result, and all of them
-    give the same bits (the K order of an output element does not depend on the tile)."""
+def test_every_mfma_tile_matches_oracle(dev, kw, kernel, monkeypatch):
+    """Each workgroup tile the library can choose (P0K_MFMA_TILE forces one) of both MFMA kernels (P0K_MFMA_KERNEL=reg
+    forces the register-staged one) gives the oracle's result, and all tiles of one kernel give the same bits (the K
+    order of an output element does not depend on the tile)."""
     c = make_case(seed=21, **kw)
     want = c.run_oracle()
+    if kernel == "mfma":
+        monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
+    elif p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] != "mfma_dma":
+        pytest.skip("the call does not qualify for the load-to-LDS kernel")
     outs = []
     for t in MFMA_TILES:
-        banner(f"tile {t} {kw}")
+        banner(f"tile {t} {kernel} {kw}")
         monkeypatch.setenv("P0K_MFMA_TILE", t)
         a = c.args(lambda n: c.bufs[n])
-        assert p0k.select_tile(a)["BM"] == int(t.split("x")[0]) and p0k.select_tile(a)["kernel"] == "mfma"
+        assert p0k.select_tile(a)["BM"] == int(t.split("x")[0]) and p0k.select_tile(a)["kernel"] == kernel
         got = c.run_device(dev)
-        assert_close(got, want, fp16=want.dtype == np.uint16, what=f"tile {t}")
+        assert_close(got, want, fp16=want.dtype == np.uint16, what=f"tile {t} {kernel}")
         outs.append(got)
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
