@@ -244,7 +244,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   if (plan) {
     plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128;
     // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
-    if (kernel == K_MFMA && gemm_dma_ok(p, we, xm)) {
+    if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes)) {
       const char *ov = getenv("P0K_MFMA_KERNEL");
       if (!ov || strcmp(ov, "reg") != 0) kernel = plan->kernel = K_MFMA_DMA;
     }

@@ -59,12 +59,13 @@ struct DT {
 __device__ __forceinline__ uint32_t lds_u32(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
-// load-to-LDS of 16 (4) bytes per lane: lane l writes LDS [m0 + 16 l] ([m0 + 4 l])
-__device__ __forceinline__ void dma16(const void *src, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
+// load-to-LDS of 16 (4) bytes per lane from the uniform base + the lane's 32-bit offset: lane l writes LDS
+// [m0 + 16 l] ([m0 + 4 l])
+__device__ __forceinline__ void dma16(const uint8_t *base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory");
 }
-__device__ __forceinline__ void dma4(const void *src, uint32_t m0) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(src) : "memory");
+__device__ __forceinline__ void dma4(const uint8_t *base, uint32_t off, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory");
 }
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14])
 template <int N>
@@ -85,14 +86,15 @@ __device__ __forceinline__ bool q4n_fast_ok(uint32_t sm) {
   return q4_fast_ok(sm) && (es >= 5u || (sm & 0x7fffu) == 0u);
 }
 // q4 code word (k0..k7, low nibble first) -> f16x8 in natural order
-__device__ __forceinline__ f16x8 dq4_fast(uint32_t w, f16x2 s2, f16x2 m2) {
+// (msk, mag: 0x00F0000F and 0x64006400 held in registers, so the mask-and-bias is one v_and_or_b32)
+__device__ __forceinline__ f16x8 dq4_fast(uint32_t w, f16x2 s2, f16x2 m2, uint32_t msk, uint32_t mag) {
   const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     // byte i to bytes 0 and 2: (q_2i | 16 q_2i+1) in both halves; the mask keeps q_2i low, 16 q_2i+1 high
     const uint32_t t = perm(w, w, 0x0c000c00u | (uint32_t)i | ((uint32_t)i << 16));
-    const uint32_t v = (t & 0x00F0000Fu) | 0x64006400u;
+    const uint32_t v = (t & msk) | mag;
     o[i] = as_u(__builtin_elementwise_fma(as_h2(v) - k1024, s2, m2));
   }
   return __builtin_bit_cast(f16x8, (u32x4){o[0], o[1], o[2], o[3]});
@@ -139,7 +141,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   constexpr int WTM = TBM / 2, WTN = TBN / 2;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint32_t mt, nt;
   tile_order(p, blockIdx.x, mt, nt);
   const uint32_t mB = mt * TBM, nB = nt * TBN;
@@ -147,7 +149,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
 
   // ---- per-lane DMA sources (step 0) and per-step advances; instruction t of this wave is number 4 t + wave of
   //      the stage's list
-  const uint8_t *src[NW];
+  uint32_t src[NW];                                   // byte offsets from X' / the weights (both < 4 GiB)
   uint32_t dst[NW];                                   // byte offset inside a stage
 #pragma unroll
   for (int t = 0; t < NW; t++) {
@@ -156,30 +158,30 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       const uint32_t r = 8 * q + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
       uint32_t m = mB + r;
       m = m < p.M ? m : p.M - 1u;
-      src[t] = p.X + ((size_t)m * p.ldx + p.kx0 + 8 * c) * 2;
+      src[t] = (m * p.ldx + p.kx0 + 8 * c) * 2u;
       dst[t] = q * 1024;
     } else if (t < T::WA + T::WC) {
       const int b = q - 4 * T::WA;
       if constexpr (WE == W_F16) {                    // weight rows of ws columns 8b .. 8b+7
         const uint32_t r = 8 * b + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
-        src[t] = p.W + ((size_t)wrow(p, nB + r) * p.wG + p.wk0 + 8 * c) * 2;
+        src[t] = (wrow(p, nB + r) * p.wG + p.wk0 + 8 * c) * 2u;
       } else if constexpr (WE == W_Q4) {              // block b / 2, record b & 1: code row of column lane
         const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
-        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + (r & 63u) * 16u;
+        src[t] = ((r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + (r & 63u) * 16u;
       } else {                                        // block b / 4, chunk b & 3
         const uint32_t r = wrow(p, nB + 64 * (b >> 2) + lane);
-        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + (r & 63u) * 64u + (b & 3) * 16u;
+        src[t] = ((r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + (r & 63u) * 64u + (b & 3) * 16u;
       }
       dst[t] = T::A_BYTES + b * 1024;
     } else {
       const int b = q - 4 * (T::WA + T::WC);
       if constexpr (WE == W_Q4) {                     // (scale, min) word of block b / 2, record b & 1
         const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
-        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + 1024u + (r & 63u) * 4u;
+        src[t] = ((r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + 1024u + (r & 63u) * 4u;
       } else if constexpr (WE == W_Q8) {              // scale pair word of block b (repeats past the last block)
         const int bb = b < T::NBLK ? b : T::NBLK - 1;
         const uint32_t r = wrow(p, nB + 64 * bb + lane);
-        src[t] = p.W + ((size_t)(r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + 4096u + (r & 62u) * 2u;
+        src[t] = ((r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + 4096u + (r & 62u) * 2u;
       }
       dst[t] = T::A_BYTES + T::BC_BYTES + b * 256;
     }
@@ -193,9 +195,9 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
 #pragma unroll
     for (int t = part * NP; t < (part + 1) * NP && t < NW; t++) {
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(smem0 + st * T::STAGE + dst[t]);
-      if (t < T::WA) dma16(src[t] + (size_t)kt * 128u, m0);
-      else if (t < T::WA + T::WC) dma16(src[t] + (size_t)kt * WSTEP, m0);
-      else dma4(src[t] + (size_t)kt * WSTEP, m0);
+      if (t < T::WA) dma16(p.X + (size_t)kt * 128u, src[t], m0);
+      else if (t < T::WA + T::WC) dma16(p.W + (size_t)kt * WSTEP, src[t], m0);
+      else dma4(p.W + (size_t)kt * WSTEP, src[t], m0);
     }
   };
 
@@ -241,31 +243,17 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       }
     }
   };
-  // decode the weight fragments of sub-step `sub` from bc / bs
+  // decode the weight fragments of sub-step `sub` from bc / bs. q4 takes the fast decode for every word here; a step
+  // whose (scale, min) words are not all fast-path words is redone by fix_q4 after the sub-step's interleaved region,
+  // so the common path stays one straight-line block.
+  bool allfast = true;
+  f16x2 qs2[BJ], qm2[BJ];                              // q4: (s, s / 16) and (mn, mn) of the step's words
+  uint32_t msk = 0x00F0000Fu, mag = 0x64006400u;
+  asm volatile("" : "+v"(msk), "+v"(mag));
   auto decode = [&](f16x8 *F, int sub) __attribute__((always_inline)) {
     if constexpr (WE == W_Q4) {
-      bool fast = true;
 #pragma unroll
-      for (int j = 0; j < BJ; j++) fast = fast && q4n_fast_ok(bs[j]);
-      if (__builtin_expect(__all(fast), 1)) {
-#pragma unroll
-        for (int j = 0; j < BJ; j++) {
-          const f16x2 sm2 = as_h2(bs[j]);
-          const f16x2 s2 = {sm2.x, sm2.x * (f16)0.0625f}, m2 = {sm2.y, sm2.y};
-          F[j] = dq4_fast(bc[j][0][sub], s2, m2);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < BJ; j++) {
-          if (q4n_fast_ok(bs[j])) {
-            const f16x2 sm2 = as_h2(bs[j]);
-            const f16x2 s2 = {sm2.x, sm2.x * (f16)0.0625f}, m2 = {sm2.y, sm2.y};
-            F[j] = dq4_fast(bc[j][0][sub], s2, m2);
-          } else {
-            F[j] = dq4_slow(bc[j][0][sub], bs[j]);
-          }
-        }
-      }
+      for (int j = 0; j < BJ; j++) F[j] = dq4_fast(bc[j][0][sub], qs2[j], qm2[j], msk, mag);
     } else if constexpr (WE == W_Q8) {
 #pragma unroll
       for (int j = 0; j < BJ; j++) {
@@ -273,6 +261,33 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
         const f16x2 s2 = as_h2(sh | (sh << 16));
         const u32x4 &c = bc[j][sub >> 1];
         F[j] = (sub & 1) ? dq8(c.z, c.w, s2) : dq8(c.x, c.y, s2);
+      }
+    }
+  };
+  auto fix_q4 = [&](f16x8 *F, int sub) __attribute__((always_inline)) {
+    if constexpr (WE == W_Q4) {
+      if (!allfast) {
+#pragma unroll
+        for (int j = 0; j < BJ; j++)
+          if (!q4n_fast_ok(bs[j])) F[j] = dq4_slow(bc[j][0][sub], bs[j]);
+      }
+    }
+  };
+  auto check_q4 = [&]() __attribute__((always_inline)) {
+    if constexpr (WE == W_Q4) {
+      bool f = true;
+#pragma unroll
+      for (int j = 0; j < BJ; j++) f = f && q4n_fast_ok(bs[j]);
+      allfast = __all(f);
+    }
+  };
+  auto scales_q4 = [&]() __attribute__((always_inline)) {
+    if constexpr (WE == W_Q4) {
+#pragma unroll
+      for (int j = 0; j < BJ; j++) {
+        const f16x2 sm2 = as_h2(bs[j]);
+        qs2[j] = (f16x2){sm2.x, sm2.x * (f16)0.0625f};
+        qm2[j] = (f16x2){sm2.y, sm2.y};
       }
     }
   };
@@ -307,7 +322,10 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
     rdB_f16(FB[0], 0, 0);
   } else {
     rdB_codes(0);
+    check_q4();
+    scales_q4();
     decode(FB[0], 0);
+    fix_q4(FB[0], 0);
   }
   int st = 0, pst = S - 1;
   uint32_t pk = S - 1;
@@ -322,6 +340,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       mfma(FA[sub & 1], FB[sub & 1]);
       sched();
       __builtin_amdgcn_sched_barrier(0);
+      fix_q4(Bn, sub + 1);
     }
     // the next stage has landed (own loads: only the refills of later stages may stay in flight), every wave is done
     // with this one (its fragments are in registers), then refill it with step kt + S
@@ -338,11 +357,16 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
     } else {
       // the last sub-step's weight fragments are decoded: the codes of the next step may replace them
       rdB_codes(sn);
+      scales_q4();
       mfma(FA[1], FB[1]);
       decode(FB[0], 0);
     }
     sched();
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (WE == W_Q4) {
+      check_q4();
+      fix_q4(FB[0], 0);
+    }
     st = sn;
   }
   wait_vm<0>();
@@ -405,8 +429,11 @@ __global__ __launch_bounds__(256) void k_xprep(Params p, uint16_t *xp) {
 
 }  // namespace
 
-bool gemm_dma_ok(const Params &p, int we, int xm) {
+bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes) {
   if (xm != X_F16 && xm != X_RMS && xm != X_LNMOD) return false;
+  // 32-bit lane offsets from the X' and weight bases
+  const uint64_t xbytes = xm == X_F16 ? ((uint64_t)p.M * p.ldx + p.kx0 + p.K) * 2 : (uint64_t)p.M * p.K * 2;
+  if (xbytes >= (1ull << 32) || wbytes >= (1ull << 32)) return false;
   if (p.K % DBK != 0 || p.K == 0) return false;
   if (xm == X_F16 && !(p.flags & F_XALIGN8)) return false;
   if (we == W_F16 && !(p.flags & F_WALIGN8)) return false;
@@ -433,9 +460,16 @@ void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsign
     if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::OCC : (m == 128 ? DT<W_Q4, 128, 256>::OCC : DT<W_Q4, 256, 128>::OCC);
     return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::OCC : (m == 128 ? DT<W_Q8, 128, 256>::OCC : DT<W_Q8, 256, 128>::OCC);
   };
-  struct C { unsigned m, n; double rate; } cand[] = {{256, 256, 1.0}, {128, 256, 0.85}, {256, 128, 0.85}, {128, 128, 0.7}};
+  // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: the quantised weights
+  // favour 256-row tiles (each decoded weight feeds four 32-row blocks instead of two)
+  struct C { unsigned m, n; double rate; };
+  const C c16[] = {{256, 256, 1.0}, {128, 256, 0.96}, {256, 128, 0.98}, {128, 128, 0.93}};
+  const C cq4[] = {{256, 256, 0.91}, {128, 256, 0.74}, {256, 128, 1.0}, {128, 128, 0.75}};
+  const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.83}, {256, 128, 0.92}, {128, 128, 0.86}};
+  const C *cand = we == W_F16 ? c16 : (we == W_Q4 ? cq4 : cq8);
   double best = -1.0;
-  for (const C &c : cand) {
+  for (int ci = 0; ci < 4; ci++) {
+    const C &c = cand[ci];
     if (c.n == 256 && N <= 128) continue;
     if (c.m == 256 && M <= 128) continue;
     const uint64_t tiles = (uint64_t)((M + c.m - 1) / c.m) * ((N + c.n - 1) / c.n), slots = (uint64_t)cus * per_cu(c.m, c.n);

@@ -13,7 +13,7 @@ hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsign
 // MFMA GEMM with load-to-LDS operands (fp16 rows of X' in memory; q4 / q8 / f16 weights decoded in registers).
 // gemm_dma_ok: the call qualifies (prologue f16 with 16-byte rows, or rms / lnmod materialised by launch_xprep into an
 // M x K fp16 buffer; K % 64 == 0). dma_tile picks the tile.
-bool gemm_dma_ok(const Params &p, int we, int xm);
+bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes);
 void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s);
 hipError_t launch_gemm_dma(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s);
