@@ -247,6 +247,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   // whose (scale, min) words are not all fast-path words is redone by fix_q4 after the sub-step's interleaved region,
   // so the common path stays one straight-line block.
   bool allfast = true;
+  uint32_t fmask = 0;                                  // q4: bit j = word j of this step takes the fast decode
   f16x2 qs2[BJ], qm2[BJ];                              // q4: (s, s / 16) and (mn, mn) of the step's words
   uint32_t msk = 0x00F0000Fu, mag = 0x64006400u;
   asm volatile("" : "+v"(msk), "+v"(mag));
@@ -269,16 +270,16 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       if (!allfast) {
 #pragma unroll
         for (int j = 0; j < BJ; j++)
-          if (!q4n_fast_ok(bs[j])) F[j] = dq4_slow(bc[j][0][sub], bs[j]);
+          if (!((fmask >> j) & 1u)) F[j] = dq4_slow(bc[j][0][sub], bs[j]);
       }
     }
   };
   auto check_q4 = [&]() __attribute__((always_inline)) {
     if constexpr (WE == W_Q4) {
-      bool f = true;
+      fmask = 0;
 #pragma unroll
-      for (int j = 0; j < BJ; j++) f = f && q4n_fast_ok(bs[j]);
-      allfast = __all(f);
+      for (int j = 0; j < BJ; j++) fmask |= (uint32_t)q4n_fast_ok(bs[j]) << j;
+      allfast = __all(fmask == (1u << BJ) - 1u);
     }
   };
   auto scales_q4 = [&]() __attribute__((always_inline)) {
