@@ -30,8 +30,14 @@
 
 namespace p0k {
 
-constexpr int GV_KSUB = 4, GV_NT = 2 * GV_KSUB * 64;     // 512 threads
-constexpr int GV_LDS = 40 * 1024;                       // X' of the slice and its group sums, then the partials
+#ifndef P0K_GV_KSUB
+#define P0K_GV_KSUB 4
+#endif
+constexpr int GV_KSUB = P0K_GV_KSUB, GV_NT = 2 * GV_KSUB * 64;     // 512 threads
+#ifndef P0K_GV_LDS_KB
+#define P0K_GV_LDS_KB 40
+#endif
+constexpr int GV_LDS = P0K_GV_LDS_KB * 1024;                       // X' of the slice and its group sums, then the partials
 
 template <int WE>
 struct Unit;
