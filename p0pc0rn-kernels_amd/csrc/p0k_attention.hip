@@ -23,7 +23,7 @@ namespace p0k {
 
 constexpr int AT_BQ = 128, AT_BK = 64, AT_NT = 256;
 
-__global__ __launch_bounds__(AT_NT) void k_attention(AttnParams p) {
+__global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
   __shared__ __attribute__((aligned(16))) f16 sK[2][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ (key & 15)
   __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ ((d >> 1) & 15)
 
@@ -109,43 +109,55 @@ __global__ __launch_bounds__(AT_NT) void k_attention(AttnParams p) {
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sacc[kb], 0, 0, 0);
       }
     }
-    // ---- scale, cap, mask (log2 domain), row max over the 64 keys
+    // ---- scores to the log2 domain: max over the raw scores (the scale is positive), then exp2(s * sl2 - m) with one
+    //      FMA per score. Soft cap: s -> cap * tanh(s * scale / cap) first. Keys past the lane's limit are masked only
+    //      in tiles that reach past some lane's limit (a wave-uniform test).
+    float sf = sl2;
     if (p.cap > 0.0f) {
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) sacc[kb][r] = p.cap * tanhf(sacc[kb][r] * p.scale / p.cap) * 1.4426950408889634f;
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++) sacc[kb] *= sl2;
+        for (int r = 0; r < 16; r++) sacc[kb][r] = p.cap * tanhf(sacc[kb][r] * p.scale / p.cap);
+      sf = 1.4426950408889634f;
     }
     const uint32_t kl = qlim > k0 ? qlim - k0 : 0u;           // keys of this tile the lane's query sees: [0, kl)
+    if (__any(kl < (uint32_t)AT_BK)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const uint32_t key = 32 * kb + 8 * (r >> 2) + 4 * gh + (r & 3);
+          sacc[kb][r] = key < kl ? sacc[kb][r] : -1.0e30f;
+        }
+    }
     float mx = -1.0e30f;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const uint32_t key = 32 * kb + 8 * (r >> 2) + 4 * gh + (r & 3);
-        const float v = key < kl ? sacc[kb][r] : -1.0e30f;
-        sacc[kb][r] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[kb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
-    m = mn;
+    // m: running maximum in the log2 domain (-1e30: none yet)
+    const float mxl = mx <= -1.0e29f ? -1.0e30f : mx * sf;
+    const float mn = fmaxf(m, mxl);
+    // a masked score (-1e30) underflows exp2 to 0; a row with no visible key yet subtracts 0 instead of -1e30
+    const float mns = mn <= -1.0e29f ? 0.0f : mn;
     float ps = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float v = sacc[kb][r];
-        const float e = v <= -1.0e29f ? 0.0f : __builtin_amdgcn_exp2f(v - mn);
+        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], sf, -mns));
         sacc[kb][r] = e;
         ps += e;
       }
-    l = l * alpha + ps;
+    if (__any(mn != m)) {                                       // rescale only when some row's maximum moved
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      l = l * alpha;
 #pragma unroll
-    for (int db = 0; db < 4; db++) oacc[db] *= alpha;
+      for (int db = 0; db < 4; db++) oacc[db] *= alpha;
+    }
+    m = mn;
+    l += ps;
 
     // ---- O^T += V^T P over four 16-key steps
 #pragma unroll
