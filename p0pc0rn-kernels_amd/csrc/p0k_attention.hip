@@ -54,24 +54,31 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
   const float sl2 = p.scale * 1.4426950408889634f;
 
   const uint16_t *Kb = p.K + (size_t)hk * p.Lk * 128, *Vb = p.V + (size_t)hk * p.Lk * 128;
-  u32x4 kr[4], vr[4];
+  u32x4 vr[4];
   const uint32_t vkg = tid & 15, vdc = tid >> 4;        // V staging: keys 4 vkg .. + 3, d 8 vdc .. + 7
+  // K goes global -> LDS by the load-to-LDS path: instruction i of wave w fills keys 4 (4 i + w) .. + 3 (1 KB), lane l
+  // the 16-byte slot l % 16 of key l / 16, i.e. logical chunk (l % 16) ^ (key & 15)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t sk0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)&sK[0][0];
+  auto kdma = [&](uint32_t t, int b) {
+    const uint32_t k0 = t * AT_BK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t kr = 4 * (4 * i + wv) + lane / 16, key = k0 + kr, c = (lane & 15) ^ (kr & 15);
+      const uint32_t off = ((key < p.Lk ? key : p.Lk - 1u) * 128 + c * 8) * 2;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(sk0 + (uint32_t)(b * AT_BK * 128 + 4 * (4 * i + wv) * 128) * 2);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(Kb) : "memory");
+    }
+  };
   auto gload = [&](uint32_t t) {
     const uint32_t k0 = t * AT_BK;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t c = tid + AT_NT * i, key = k0 + c / 16;
-      kr[i] = *(const u32x4 *)(Kb + (size_t)(key < p.Lk ? key : p.Lk - 1u) * 128 + (c % 16) * 8);
       const uint32_t vk = k0 + 4 * vkg + i;
       vr[i] = *(const u32x4 *)(Vb + (size_t)(vk < p.Lk ? vk : p.Lk - 1u) * 128 + vdc * 8);
     }
   };
   auto lstore = [&](int b) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t c = tid + AT_NT * i, key = c / 16, ch = c % 16;
-      *(u32x4 *)(sK[b] + key * 128 + ((ch ^ (key & 15u)) * 8)) = kr[i];
-    }
     const uint16_t *v0 = (const uint16_t *)&vr[0], *v1 = (const uint16_t *)&vr[1], *v2 = (const uint16_t *)&vr[2],
                    *v3 = (const uint16_t *)&vr[3];
 #pragma unroll
@@ -88,14 +95,19 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
   float m = -1.0e30f, l = 0.0f;
 
   if (ntile) {
+    kdma(0, 0);
     gload(0);
     lstore(0);
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);                     // vmcnt(0): this wave's K rows have landed
   __syncthreads();
   for (uint32_t t = 0; t < ntile; t++) {
     const int b = t & 1;
     const uint32_t k0 = t * AT_BK;
-    if (t + 1 < ntile) gload(t + 1);
+    if (t + 1 < ntile) {
+      gload(t + 1);
+      kdma(t + 1, b ^ 1);                                   // the other K buffer: every wave left it at the last barrier
+    }
 
     // ---- S^T for keys k0 .. k0+63: two 32-key blocks
     f32x16 sacc[2];
@@ -177,6 +189,7 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
       }
     }
     if (t + 1 < ntile) lstore(b ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0f70);                   // vmcnt(0): the next K tile has landed
     __syncthreads();
   }
 
