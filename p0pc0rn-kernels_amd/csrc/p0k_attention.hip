@@ -15,17 +15,23 @@
 // to one P.V step are exactly the keys its S^T registers hold, so P never leaves the registers; V is staged in LDS
 // transposed ([d][key]) so those keys are two 8-byte reads. Keys come in tiles of 64 through double-buffered LDS (the
 // next tile's global loads are issued before this tile's MFMAs); both LDS tiles are XOR-swizzled so the 16-byte K reads
-// and the 8-byte V reads of a wave hit distinct banks.
+// and the 8-byte V reads of a wave hit distinct banks (the V swizzle also folds in d >> 5, so the rows d and d + 32 that
+// one read instruction pairs land in different banks). K arrives by the load-to-LDS path; V is transposed through
+// registers. Two waves per SIMD (256 registers each) let one wave's softmax run under the other's MFMAs.
 #include "p0k_device.h"
 #include "p0k_launch.h"
 
 namespace p0k {
 
-constexpr int AT_BQ = 128, AT_BK = 64, AT_NT = 256;
+#ifndef P0K_AT_BQ
+#define P0K_AT_BQ 128
+#endif
+constexpr int AT_BQ = P0K_AT_BQ, AT_BK = 64, AT_NT = 2 * AT_BQ, AT_NW = AT_NT / 64;   // 32 queries per wave
 
-__global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
+template <bool CAP>
+__global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams p) {
   __shared__ __attribute__((aligned(16))) f16 sK[2][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ (key & 15)
-  __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ ((d >> 1) & 15)
+  __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ (((d >> 1) ^ (d >> 5)) & 15)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, gh = lane >> 5, l32 = lane & 31;
   const uint32_t h = blockIdx.y, hk = h / (p.Hq / p.Hkv);
@@ -54,8 +60,10 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
   const float sl2 = p.scale * 1.4426950408889634f;
 
   const uint16_t *Kb = p.K + (size_t)hk * p.Lk * 128, *Vb = p.V + (size_t)hk * p.Lk * 128;
-  u32x4 vr[4];
-  const uint32_t vkg = tid & 15, vdc = tid >> 4;        // V staging: keys 4 vkg .. + 3, d 8 vdc .. + 7
+  // V staging: thread (vkg, vdc, vh) holds keys 4 vkg + VPT vh .. + VPT-1 of d 8 vdc .. + 7
+  constexpr int VPT = 4 * 256 / AT_NT;                   // keys per thread
+  u32x4 vr[VPT];
+  const uint32_t vkg = tid & 15, vdc = (tid >> 4) & 15, vh = tid >> 8;
   // K goes global -> LDS by the load-to-LDS path: instruction i of wave w fills keys 4 (4 i + w) .. + 3 (1 KB), lane l
   // the 16-byte slot l % 16 of key l / 16, i.e. logical chunk (l % 16) ^ (key & 15)
   const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -63,31 +71,48 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
   auto kdma = [&](uint32_t t, int b) {
     const uint32_t k0 = t * AT_BK;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t kr = 4 * (4 * i + wv) + lane / 16, key = k0 + kr, c = (lane & 15) ^ (kr & 15);
+    for (int i = 0; i < 16 / AT_NW; i++) {
+      const uint32_t kr = 4 * (AT_NW * i + wv) + lane / 16, key = k0 + kr, c = (lane & 15) ^ (kr & 15);
       const uint32_t off = ((key < p.Lk ? key : p.Lk - 1u) * 128 + c * 8) * 2;
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(sk0 + (uint32_t)(b * AT_BK * 128 + 4 * (4 * i + wv) * 128) * 2);
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(sk0 + (uint32_t)(b * AT_BK * 128 + 4 * (AT_NW * i + wv) * 128) * 2);
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(Kb) : "memory");
     }
   };
   auto gload = [&](uint32_t t) {
     const uint32_t k0 = t * AT_BK;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t vk = k0 + 4 * vkg + i;
+    for (int i = 0; i < VPT; i++) {
+      const uint32_t vk = k0 + 4 * vkg + VPT * vh + i;
       vr[i] = *(const u32x4 *)(Vb + (size_t)(vk < p.Lk ? vk : p.Lk - 1u) * 128 + vdc * 8);
     }
   };
   auto lstore = [&](int b) {
-    const uint16_t *v0 = (const uint16_t *)&vr[0], *v1 = (const uint16_t *)&vr[1], *v2 = (const uint16_t *)&vr[2],
-                   *v3 = (const uint16_t *)&vr[3];
+    if constexpr (VPT == 4) {
+      // The 16 threads of one d cover the 16 units of its row (half the banks), so the two d a 32-lane half writes
+      // per instruction must differ in parity (row parity picks the bank half): odd 16-lane groups write the rows
+      // of each pair (2w, 2w+1) in swapped order, picking the halves with a lane-dependent v_perm selector.
+      const uint32_t odd = (tid >> 4) & 1u;
+      const uint32_t s0 = odd ? 0x07060302u : 0x05040100u, s1 = odd ? 0x05040100u : 0x07060302u;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const uint32_t d = vdc * 8 + j;
-      *(u32x2 *)(sV[b] + d * AT_BK + ((vkg ^ ((d >> 1) & 15u)) * 4)) =
-          (u32x2){(uint32_t)v0[j] | ((uint32_t)v1[j] << 16), (uint32_t)v2[j] | ((uint32_t)v3[j] << 16)};
+      for (int w = 0; w < 4; w++) {
+        const uint32_t a0 = vr[0][w], a1 = vr[1][w], a2 = vr[2][w], a3 = vr[3][w];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t sel = h ? s1 : s0, d = vdc * 8 + 2 * w + (h ^ odd);
+          *(u32x2 *)(sV[b] + d * AT_BK + ((vkg ^ (((d >> 1) ^ (d >> 5)) & 15u)) * 4)) = (u32x2){perm(a1, a0, sel), perm(a3, a2, sel)};
+        }
+      }
+    } else {                                               // two keys per thread: half of a 4-key unit
+      const uint16_t *v0 = (const uint16_t *)&vr[0], *v1 = (const uint16_t *)&vr[1];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t d = vdc * 8 + j;
+        *(uint32_t *)(sV[b] + d * AT_BK + ((vkg ^ (((d >> 1) ^ (d >> 5)) & 15u)) * 4) + 2 * vh) =
+            (uint32_t)v0[j] | ((uint32_t)v1[j] << 16);
+      }
     }
   };
+
 
   f32x16 oacc[4];
 #pragma unroll
@@ -125,7 +150,7 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
     //      FMA per score. Soft cap: s -> cap * tanh(s * scale / cap) first. Keys past the lane's limit are masked only
     //      in tiles that reach past some lane's limit (a wave-uniform test).
     float sf = sl2;
-    if (p.cap > 0.0f) {
+    if constexpr (CAP) {
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -181,7 +206,7 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
       const uint32_t u1 = 8 * kb + 4 * h2 + gh, u2 = u1 + 2;   // 4-key units of the lane's 8 keys
 #pragma unroll
       for (int db = 0; db < 4; db++) {
-        const uint32_t d = 32 * db + l32, sw = (d >> 1) & 15u;
+        const uint32_t d = 32 * db + l32, sw = ((d >> 1) ^ (d >> 5)) & 15u;
         const u32x2 lo = *(const u32x2 *)(sV[b] + d * AT_BK + ((u1 ^ sw) * 4));
         const u32x2 hi = *(const u32x2 *)(sV[b] + d * AT_BK + ((u2 ^ sw) * 4));
         const f16x8 av = __builtin_bit_cast(f16x8, (u32x4){lo.x, lo.y, hi.x, hi.y});
@@ -212,7 +237,8 @@ __global__ __launch_bounds__(AT_NT, 2) void k_attention(AttnParams p) {
 hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
   if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
   dim3 grid((p.Lq + AT_BQ - 1) / AT_BQ, p.Hq);
-  hipLaunchKernelGGL(k_attention, grid, dim3(AT_NT), 0, s, p);
+  if (p.cap > 0.0f) hipLaunchKernelGGL(k_attention<true>, grid, dim3(AT_NT), 0, s, p);
+  else hipLaunchKernelGGL(k_attention<false>, grid, dim3(AT_NT), 0, s, p);
   return hipGetLastError();
 }
 
