@@ -176,6 +176,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
           frames = (uint64_t)(hi - p.padL + 1);
         }
         FITS("x", a->x_off + frames * p.Hi * p.Wi * p.Ci * 2, xav);
+        p.nvox = frames * p.Hi * p.Wi < (1ull << 32) ? (uint32_t)(frames * p.Hi * p.Wi) : 0xffffffffu;
         if (a->c_pn) FITS("stats", frames * p.Hi * p.Wi * 4, a->st_size);
       }
     }

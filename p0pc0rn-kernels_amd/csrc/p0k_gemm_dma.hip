@@ -61,10 +61,21 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p) {
 }
 // load-to-LDS of 16 (4) bytes per lane from the uniform base + the lane's 32-bit offset: lane l writes LDS
 // [m0 + 16 l] ([m0 + 4 l])
+// a wave-uniform pointer in SGPRs (the "s" constraint does not move a value the compiler keeps in VGPRs)
+__device__ __forceinline__ const uint8_t *sgpr_ptr(const uint8_t *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void dma16(const uint8_t *base, uint32_t off, uint32_t m0) {
+  base = sgpr_ptr(base);
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory");
 }
+__device__ __forceinline__ void dma16a(const uint8_t *addr, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(addr) : "memory");
+}
 __device__ __forceinline__ void dma4(const uint8_t *base, uint32_t off, uint32_t m0) {
+  base = sgpr_ptr(base);
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(off), "s"(base) : "memory");
 }
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14])
@@ -133,7 +144,8 @@ __device__ __forceinline__ void tile_order(const Params &p, uint32_t bid, uint32
   nt = in / rows;
 }
 
-template <int WE, int TBM, int TBN>
+// XG: X' rows (X_F16: an fp16 matrix) or the conv3 gather (X_CONV3: input voxels [vox][Ci], padding taps read Z)
+template <int WE, int XG, int TBM, int TBN>
 __global__ __launch_bounds__(DNT, (DT<WE, TBM, TBN>::OCC))
 __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::OCC)))) void k_gemm_dma(Params p) {
   using T = DT<WE, TBM, TBN>;
@@ -150,6 +162,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   // ---- per-lane DMA sources (step 0) and per-step advances; instruction t of this wave is number 4 t + wave of
   //      the stage's list
   uint32_t src[NW];                                   // byte offsets from X' / the weights (both < 4 GiB)
+  uint32_t cv_it[XG == X_CONV3 ? T::WA : 1], cv_yx[XG == X_CONV3 ? T::WA : 1];   // conv3 row contexts
   uint32_t dst[NW];                                   // byte offset inside a stage
 #pragma unroll
   for (int t = 0; t < NW; t++) {
@@ -158,7 +171,23 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       const uint32_t r = 8 * q + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
       uint32_t m = mB + r;
       m = m < p.M ? m : p.M - 1u;
-      src[t] = (m * p.ldx + p.kx0 + 8 * c) * 2u;
+      if constexpr (XG == X_CONV3) {
+        // (oy | ox << 16) and the input frame of each of the three time taps (10 bits each)
+        const RowCtx rc = row_ctx<X_CONV3>(p, m);
+        uint32_t itp = 0;
+#pragma unroll
+        for (int kt3 = 0; kt3 < 3; kt3++) {
+          int itg = rc.a + (int)p.padT + kt3 - 1;
+          itg = itg < 0 ? 0 : (itg > (int)p.stride - 1 ? (int)p.stride - 1 : itg);
+          const uint32_t it = p.ks > 1u ? (uint32_t)itg % p.ks : (uint32_t)itg - p.padL;
+          itp |= it << (10 * kt3);
+        }
+        cv_it[t] = itp;
+        cv_yx[t] = (uint32_t)rc.b | ((uint32_t)rc.c << 16);
+        src[t] = 8 * c;
+      } else {
+        src[t] = (m * p.ldx + p.kx0 + 8 * c) * 2u;
+      }
       dst[t] = q * 1024;
     } else if (t < T::WA + T::WC) {
       const int b = q - 4 * T::WA;
@@ -192,10 +221,25 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   constexpr int NP = (NW + 2) / 3;
   auto issue = [&](uint32_t kt, int st, int part) __attribute__((always_inline)) {
     kt = kt < nk ? kt : nk - 1u;
+    // conv3: the step's tap (uniform; Ci % 64 == 0, so a 64-k step stays inside one tap)
+    uint32_t c0 = 0, kt3 = 0, ky = 0, kx = 0;
+    if constexpr (XG == X_CONV3) {
+      const uint32_t kg = kt * DBK, tap = kg / p.Ci, r9 = tap % 9u;
+      c0 = kg - tap * p.Ci;
+      kt3 = tap / 9u;
+      ky = r9 / 3u;
+      kx = r9 - 3u * ky;
+    }
 #pragma unroll
     for (int t = part * NP; t < (part + 1) * NP && t < NW; t++) {
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(smem0 + st * T::STAGE + dst[t]);
-      if (t < T::WA) dma16(p.X + (size_t)kt * 128u, src[t], m0);
+      if (XG == X_CONV3 && t < T::WA) {
+        const uint32_t it = (cv_it[t] >> (10 * kt3)) & 1023u;
+        const int iy = (int)(cv_yx[t] & 0xffffu) + (int)ky - 1, ix = (int)(cv_yx[t] >> 16) + (int)kx - 1;
+        const bool in = (uint32_t)iy < p.Hi && (uint32_t)ix < p.Wi;
+        const size_t vox = ((size_t)it * p.Hi + (uint32_t)iy) * p.Wi + (uint32_t)ix;
+        dma16a(in ? p.X + (vox * p.Ci + c0) * 2 + src[t] * 2 : p.Z, m0);
+      } else if (t < T::WA) dma16(p.X + (size_t)kt * 128u, src[t], m0);
       else if (t < T::WA + T::WC) dma16(p.W + (size_t)kt * WSTEP, src[t], m0);
       else dma4(p.W + (size_t)kt * WSTEP, src[t], m0);
     }
@@ -399,22 +443,38 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
     }
 }
 
-template <int WE, int TBM, int TBN>
+template <int WE, int XG, int TBM, int TBN>
 hipError_t launch_dma_one(const Params &p, hipStream_t s) {
   Params q = p;
   q.tilesM = (p.M + TBM - 1) / TBM;
   q.tilesN = (p.N + TBN - 1) / TBN;
-  hipLaunchKernelGGL((k_gemm_dma<WE, TBM, TBN>), dim3(q.tilesM * q.tilesN), dim3(DNT), 0, s, q);
+  hipLaunchKernelGGL((k_gemm_dma<WE, XG, TBM, TBN>), dim3(q.tilesM * q.tilesN), dim3(DNT), 0, s, q);
   return hipGetLastError();
 }
 
-template <int WE>
+template <int WE, int XG>
 hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
-  if (bm == 256 && bn == 256) return launch_dma_one<WE, 256, 256>(p, s);
-  if (bm == 256 && bn == 128) return launch_dma_one<WE, 256, 128>(p, s);
-  if (bm == 128 && bn == 256) return launch_dma_one<WE, 128, 256>(p, s);
-  if (bm == 128 && bn == 128) return launch_dma_one<WE, 128, 128>(p, s);
+  if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256>(p, s);
+  if (bm == 256 && bn == 128) return launch_dma_one<WE, XG, 256, 128>(p, s);
+  if (bm == 128 && bn == 256) return launch_dma_one<WE, XG, 128, 256>(p, s);
+  if (bm == 128 && bn == 128) return launch_dma_one<WE, XG, 128, 128>(p, s);
   return hipErrorInvalidValue;
+}
+
+// conv3 PixelNorm + SiLU, materialised once per input element (the fused prologue's exact fp16 values, xload8)
+__global__ __launch_bounds__(256) void k_pnprep(Params p, uint16_t *xp) {
+  const uint32_t c8 = p.Ci / 8;
+  const uint64_t n = (uint64_t)p.nvox * c8;
+  for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < n; t += (uint64_t)gridDim.x * 256) {
+    const uint64_t vox = t / c8;
+    const uint32_t c0 = (uint32_t)(t - vox * c8) * 8;
+    u32x4 v = *(const u32x4 *)(p.X + (vox * p.Ci + c0) * 2);
+    const float sc = p.ST[vox];
+    const f16x2 a = as_h2(v.x), b = as_h2(v.y), c = as_h2(v.z), d = as_h2(v.w);
+    v = (u32x4){pack2(silu((float)a.x * sc), silu((float)a.y * sc)), pack2(silu((float)b.x * sc), silu((float)b.y * sc)),
+                pack2(silu((float)c.x * sc), silu((float)c.y * sc)), pack2(silu((float)d.x * sc), silu((float)d.y * sc))};
+    *(u32x4 *)(xp + vox * p.Ci + c0) = v;
+  }
 }
 
 // X' of the rms / lnmod prologues, materialised once: Xp[m][k] = xload8 (the fused prologue's exact values)
@@ -431,10 +491,17 @@ __global__ __launch_bounds__(256) void k_xprep(Params p, uint16_t *xp) {
 }  // namespace
 
 bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes) {
-  if (xm != X_F16 && xm != X_RMS && xm != X_LNMOD) return false;
-  // 32-bit lane offsets from the X' and weight bases
-  const uint64_t xbytes = xm == X_F16 ? ((uint64_t)p.M * p.ldx + p.kx0 + p.K) * 2 : (uint64_t)p.M * p.K * 2;
-  if (xbytes >= (1ull << 32) || wbytes >= (1ull << 32)) return false;
+  if (xm != X_F16 && xm != X_RMS && xm != X_LNMOD && xm != X_CONV3) return false;
+  if (xm == X_CONV3) {
+    // 64-k steps inside one tap; input frames of the three time taps packed in 10 bits; (oy, ox) in 16
+    if (p.Ci % 64 != 0 || p.stride > 1024 || p.ks > 1024 || p.Ho > 65535 || p.Wo > 65535 || p.nvox == 0xffffffffu)
+      return false;
+  } else {
+    // 32-bit lane offsets from the X' base
+    const uint64_t xbytes = xm == X_F16 ? ((uint64_t)p.M * p.ldx + p.kx0 + p.K) * 2 : (uint64_t)p.M * p.K * 2;
+    if (xbytes >= (1ull << 32)) return false;
+  }
+  if (wbytes >= (1ull << 32)) return false;
   if (p.K % DBK != 0 || p.K == 0) return false;
   if (xm == X_F16 && !(p.flags & F_XALIGN8)) return false;
   if (we == W_F16 && !(p.flags & F_WALIGN8)) return false;
@@ -444,6 +511,12 @@ bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes) {
 }
 
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
+  if (xm == X_CONV3) {
+    const uint64_t n = (uint64_t)p.nvox * (p.Ci / 8);
+    const unsigned blocks = (unsigned)(n / 256 < 4096 ? (n + 255) / 256 : 4096);
+    if (n) hipLaunchKernelGGL(k_pnprep, dim3(blocks), dim3(256), 0, s, p, xp);
+    return hipGetLastError();
+  }
   const uint64_t n = (uint64_t)p.M * (p.K / 8);
   const unsigned blocks = (unsigned)(n / 256 < 4096 ? (n + 255) / 256 : 4096);
   if (xm == X_RMS) hipLaunchKernelGGL(k_xprep<X_RMS>, dim3(blocks), dim3(256), 0, s, p, xp);
@@ -481,11 +554,19 @@ void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsign
   }
 }
 
-hipError_t launch_gemm_dma(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s) {
+hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s) {
+  if (xg == X_CONV3) {
+    switch (we) {
+    case W_Q4: return launch_dma_we<W_Q4, X_CONV3>(p, bm, bn, s);
+    case W_Q8: return launch_dma_we<W_Q8, X_CONV3>(p, bm, bn, s);
+    case W_F16: return launch_dma_we<W_F16, X_CONV3>(p, bm, bn, s);
+    }
+    return hipErrorInvalidValue;
+  }
   switch (we) {
-  case W_Q4: return launch_dma_we<W_Q4>(p, bm, bn, s);
-  case W_Q8: return launch_dma_we<W_Q8>(p, bm, bn, s);
-  case W_F16: return launch_dma_we<W_F16>(p, bm, bn, s);
+  case W_Q4: return launch_dma_we<W_Q4, X_F16>(p, bm, bn, s);
+  case W_Q8: return launch_dma_we<W_Q8, X_F16>(p, bm, bn, s);
+  case W_F16: return launch_dma_we<W_F16, X_F16>(p, bm, bn, s);
   }
   return hipErrorInvalidValue;
 }

@@ -10,13 +10,14 @@ constexpr unsigned MI355X_CUS = 256;
 // MFMA GEMM (any M): bm x bn tiles in {128, 256}^2, 512 threads; mfma_tile picks the tile for a shape
 void mfma_tile(uint32_t M, uint32_t N, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsigned bn, hipStream_t s);
-// MFMA GEMM with load-to-LDS operands (fp16 rows of X' in memory; q4 / q8 / f16 weights decoded in registers).
-// gemm_dma_ok: the call qualifies (prologue f16 with 16-byte rows, or rms / lnmod materialised by launch_xprep into an
-// M x K fp16 buffer; K % 64 == 0). dma_tile picks the tile.
+// MFMA GEMM with load-to-LDS operands (fp16 rows of X' in memory, or the conv3 gather of input voxels; q4 / q8 / f16
+// weights decoded in registers). gemm_dma_ok: the call qualifies (prologue f16 with 16-byte rows, rms / lnmod
+// materialised by launch_xprep into an M x K fp16 buffer, or conv3 with Ci % 64 == 0, its PixelNorm materialised by
+// launch_xprep over the input voxels; K % 64 == 0). dma_tile picks the tile. xg: X_F16 (rows) or X_CONV3.
 bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes);
 void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s);
-hipError_t launch_gemm_dma(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s);
+hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
 // (part: S*M*N floats, cnt: one zeroed counter per 128-column tile). mf: the matrix-core variant (2 <= M <= 16).
 void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S, unsigned *KS);

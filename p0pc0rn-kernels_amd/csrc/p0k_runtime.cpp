@@ -59,6 +59,8 @@ struct p0k_ctx {
   // X' of the rms / lnmod prologues for the load-to-LDS GEMM (M x K fp16, grown on demand)
   void *ws_x = nullptr;
   uint64_t ws_x_bytes = 0;
+  // 256 zero bytes: the padding taps of the load-to-LDS conv3 gather read them
+  void *ws_zero = nullptr;
 };
 
 struct p0k_event { hipEvent_t ev; int device; };
@@ -85,7 +87,15 @@ int p0k_ctx_create(int device, p0k_ctx **out) {
   if (e != hipSuccess) { delete c; return hip_err(e, "hipStreamCreate"); }
   e = hipMalloc((void **)&c->ws_cnt, sizeof(uint32_t) * p0k_ctx::WS_COUNTERS);
   if (e == hipSuccess) e = hipMemset(c->ws_cnt, 0, sizeof(uint32_t) * p0k_ctx::WS_COUNTERS);
-  if (e != hipSuccess) { (void)hipStreamDestroy(c->stream); delete c; return hip_err(e, "workspace counters"); }
+  if (e == hipSuccess) e = hipMalloc(&c->ws_zero, 256);
+  if (e == hipSuccess) e = hipMemset(c->ws_zero, 0, 256);
+  if (e != hipSuccess) {
+    if (c->ws_cnt) (void)hipFree(c->ws_cnt);
+    if (c->ws_zero) (void)hipFree(c->ws_zero);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return hip_err(e, "workspace counters");
+  }
   *out = c;
   return P0K_OK;
 }
@@ -99,6 +109,7 @@ void p0k_ctx_destroy(p0k_ctx *c) {
     for (auto &b : kv.second) (void)hipFree(b.ptr);
   if (c->ws_part) (void)hipFree(c->ws_part);
   if (c->ws_x) (void)hipFree(c->ws_x);
+  if (c->ws_zero) (void)hipFree(c->ws_zero);
   if (c->ws_cnt) (void)hipFree(c->ws_cnt);
   (void)hipStreamDestroy(c->stream);
   delete c;
@@ -347,6 +358,17 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
       if (int rr = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "decode")) return rr;
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF);
+  } else if (plan.kernel == p0k::K_MFMA_DMA && plan.xm == P0K_X_CONV3) {
+    p.Z = (const uint8_t *)c->ws_zero;
+    if (p.flags & p0k::F_PN) {
+      // PixelNorm + SiLU once per input element into the X' workspace; the gather then reads plain fp16 voxels
+      const uint64_t need = (uint64_t)p.nvox * p.Ci * 2u;
+      if (int rr = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return rr;
+      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)c->ws_x, c->stream);
+      if (e != hipSuccess) return hip_err(e, "gemm prologue launch");
+      p.X = (const uint8_t *)c->ws_x;
+    }
+    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_CONV3, plan.bm, plan.bn, c->stream);
   } else if (plan.kernel == p0k::K_MFMA_DMA) {
     if (plan.xm != P0K_X_F16) {
       // the prologue once per element into the X' workspace; the GEMM then reads fp16 rows
@@ -358,7 +380,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
       p.ldx = a->K;
       p.kx0 = 0;
     }
-    e = p0k::launch_gemm_dma(p, plan.we, plan.bm, plan.bn, c->stream);
+    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_F16, plan.bm, plan.bn, c->stream);
   } else {
     e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, plan.bm, plan.bn, c->stream);
   }

@@ -173,7 +173,7 @@ def _conv3_call(dev, c, dw, xbuf, xoff, ybuf, yoff, t0, nf, padL=0, ks=1):
                        "padL": padL, "ks": ks}})
 
 
-@pytest.mark.parametrize("dims", [(5, 6, 6, 32, 128), (7, 5, 9, 64, 64)])
+@pytest.mark.parametrize("dims", [(5, 6, 6, 32, 128), (7, 5, 9, 64, 64), (4, 6, 10, 128, 128)])
 def test_conv3_chunks_and_ring_bit_identical(dev, dims):
     """test/kernels.test.js:123-145: 2-frame chunks and a 3-frame ring give output bit-identical to the whole clip."""
     T, H, W, C, N = dims
@@ -201,9 +201,30 @@ def test_conv3_chunks_and_ring_bit_identical(dev, dims):
             dev.free(b)
 
 
-def test_conv3_pixelnorm(dev):
-    c = make_conv3_case(pn=True)
-    assert_close(c.run_device(dev), c.run_oracle(), what="conv3 pn")
+@pytest.mark.parametrize("C", [32, 128])
+def test_conv3_pixelnorm(dev, C):
+    c = make_conv3_case(C=C, pn=True)
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("mfma_dma" if C % 64 == 0 else "mfma")
+    assert_close(c.run_device(dev), c.run_oracle(), what=f"conv3 pn C={C}")
+
+
+@pytest.mark.parametrize("enc", ["f16", "q8g64s.t64"])
+@pytest.mark.parametrize("pn", [False, True])
+def test_conv3_gather_every_tile(dev, enc, pn, monkeypatch):
+    """The load-to-LDS conv3 gather (Ci % 64 == 0; padding taps read a zero block, PixelNorm materialised once per
+    input element): every tile matches the oracle and all tiles give the same bits."""
+    c = make_conv3_case(T=3, H=10, W=12, C=64, N=256, pn=pn, enc=enc)
+    want = c.run_oracle()
+    outs = []
+    for t in MFMA_TILES:
+        banner(f"conv3 gather tile {t} enc {enc} pn {pn}")
+        monkeypatch.setenv("P0K_MFMA_TILE", t)
+        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
+        got = c.run_device(dev)
+        assert_close(got, want, what=f"conv3 gather tile {t}")
+        outs.append(got)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
 
 
 @pytest.mark.parametrize("kw", [dict(), dict(stride=2), dict(up2=True), dict(gn=True), dict(ks=1, pad=0),
