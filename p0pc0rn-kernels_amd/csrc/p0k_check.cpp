@@ -249,7 +249,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       const char *ov = getenv("P0K_MFMA_KERNEL");
       if (!ov || strcmp(ov, "reg") != 0) kernel = plan->kernel = K_MFMA_DMA;
     }
-    if (kernel == K_MFMA_DMA) dma_tile(M, N, we, MI355X_CUS, &plan->bm, &plan->bn);
+    if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, MI355X_CUS, &plan->bm, &plan->bn);
     if (kernel == K_MFMA) mfma_tile(M, N, MI355X_CUS, &plan->bm, &plan->bn);
     if (kernel == K_MFMA || kernel == K_MFMA_DMA) {
       // tuning / test override of the tile (P0K_MFMA_TILE=256x128); results do not depend on it

@@ -527,7 +527,7 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 
 // The tile: each candidate scored by its relative per-CU rate times the fraction of workgroup slots (one or two per
 // CU, as the tile's LDS allows) that hold real work over the rounds the grid needs.
-void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsigned *bn) {
+void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn) {
   auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
     if (m == 256 && n == 256) return 1;
     if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::OCC) : (DT<W_F16, 128, 256>::OCC);
@@ -540,7 +540,10 @@ void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsign
   const C c16[] = {{256, 256, 1.0}, {128, 256, 0.96}, {256, 128, 0.98}, {128, 128, 0.93}};
   const C cq4[] = {{256, 256, 0.91}, {128, 256, 0.74}, {256, 128, 1.0}, {128, 128, 0.75}};
   const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.83}, {256, 128, 0.92}, {128, 128, 0.86}};
-  const C *cand = we == W_F16 ? c16 : (we == W_Q4 ? cq4 : cq8);
+  // the conv3 gather computes each row's tap address per step: two workgroups of 128 x 128 per CU hide it best
+  // (f16 weights, 13 x 92 x 160 x 128 clip: 128 x 128 252 us, 256 x 128 272, 256 x 256 382, 128 x 256 409)
+  const C cg[] = {{256, 256, 0.66}, {128, 256, 0.62}, {256, 128, 0.93}, {128, 128, 1.0}};
+  const C *cand = xg == X_CONV3 ? cg : (we == W_F16 ? c16 : (we == W_Q4 ? cq4 : cq8));
   double best = -1.0;
   for (int ci = 0; ci < 4; ci++) {
     const C &c = cand[ci];

@@ -15,7 +15,7 @@ hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsign
 // materialised by launch_xprep into an M x K fp16 buffer, or conv3 with Ci % 64 == 0, its PixelNorm materialised by
 // launch_xprep over the input voxels; K % 64 == 0). dma_tile picks the tile. xg: X_F16 (rows) or X_CONV3.
 bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes);
-void dma_tile(uint32_t M, uint32_t N, int we, unsigned cus, unsigned *bm, unsigned *bn);
+void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s);
 hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
