@@ -231,7 +231,8 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
     if ((we != P0K_ENC_Q8G64S_T64 || a->wk0 % 64 == 0) && (we != P0K_ENC_F16 || (f & F_WALIGN8)) &&
         wbytes < (1ull << 32)) {
       // one row: the VALU stream (exact dot products of fp32-dequantised weights); 2..16 rows: the matrix cores
-      const bool mf = M >= 2;
+      bool mf = M >= 2;
+      if (const char *ov = getenv("P0K_GEMV_MF")) mf = mf && atoi(ov) != 0;   // tuning: the VALU stream for M > 1
       gemv_split(p, we, MI355X_CUS, mf, &S, &KS);
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
       if (const char *ov = getenv("P0K_GEMV_SLICES")) {

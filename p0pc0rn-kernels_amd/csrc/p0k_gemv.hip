@@ -308,13 +308,16 @@ template <>
 struct MUnit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
 
 constexpr int MF_KSM = 4096;                                // longest K slice of one item
-constexpr int MF_XG = 16 * MF_KSM * 2 + 16 * (MF_KSM / 32) * 8;    // X' of 16 rows + (G1, G2) per row and group
+// X' rows are MF_KSM + 8 halfs apart: the 16 rows an MFMA A read touches then start 4 banks apart instead of all in
+// one bank (8 KB rows)
+constexpr int MF_KSP = MF_KSM + 8;
+constexpr int MF_XG = 16 * MF_KSP * 2 + 16 * (MF_KSM / 32) * 8;    // X' of 16 rows + (G1, G2) per row and group
 constexpr int MF_LDS = MF_XG + 8 * 64 * 20;                 // + per wave: one q4 unit (64 rows x 16 B) and its scales
 
 template <int WE, int XM>
 __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
   constexpr int MT = 16;
-  constexpr int UK = MUnit<WE>::UK, PF = MUnit<WE>::PF, KSM = MF_KSM;
+  constexpr int UK = MUnit<WE>::UK, PF = MUnit<WE>::PF, KSM = MF_KSP;   // KSM: the X' row stride
   static_assert(GV_KSUB * MT * 128 * 4 <= MF_LDS, "partials must fit the staging buffer");
   __shared__ __attribute__((aligned(16))) uint8_t smem[MF_LDS];
   __shared__ uint32_t sLast;
