@@ -381,10 +381,13 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   f32x4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) acc[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  // A rows past M are not staged: the lanes of those rows AND their (unwritten) LDS words with 0
+  const uint32_t am = l16 < (int)p.M ? 0xffffffffu : 0u;
+  const u32x4 amask = (u32x4){am, am, am, am};
 
   auto compute = [&](const MUnit<WE> &u, uint32_t unit) {
     if constexpr (WE == W_F16) {
-      const f16x8 a = *(const f16x8 *)(sX + l16 * KSM + unit * UK + kc * 8);
+      const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + kc * 8) & amask);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const f16x8 b = __builtin_bit_cast(f16x8, u.v[i]);
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       }
 #pragma unroll
       for (int h = 0; h < UK / 32; h++) {
-        const f16x8 a = *(const f16x8 *)(sX + l16 * KSM + unit * UK + h * 32 + kc * 8);
+        const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + h * 32 + kc * 8) & amask);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           u32x4 bw;
@@ -450,42 +453,34 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   for (int j = 0; j < PF; j++)
     if ((uint32_t)j < nuw) load(ring[j], u0 + j);
 
-  // X' of the slice -> LDS (rows past M are zero); q4: the high-nibble positions (odd pair slots) hold x / 16
-  const uint32_t nb = KS / 8, ng = KS / UK;
-  for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
-    uint32_t m = t / nb, kq = t - m * nb;
-    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-    if (m < p.M) v = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq));
-    *(u32x4 *)(sX + m * KSM + 8 * kq) = v;
-  }
-  if constexpr (WE != W_F16) {
-    __syncthreads();
-    // per (row, unit): sums of the unscaled X' over the low / high positions -> (G1, G2); then scale the q4 high slots
-    for (uint32_t t = tid; t < MT * ng; t += GV_NT) {
-      uint32_t g = t / MT, m = t - g * MT;
-      const u32x4 *x4 = (const u32x4 *)(sX + m * KSM + g * UK);
+  // X' of the slice -> LDS for the rows < M only (the MFMA A reads of rows past M take zeros instead); one thread per
+  // (row, unit) stages the unit's chunks and its sums of the unscaled X' over the low / high positions -> (G1, G2);
+  // q4: the high-nibble positions (odd pair slots) are stored as x / 16
+  const uint32_t nb = KS / 8, ng = KS / UK, Mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+  if constexpr (WE == W_F16) {
+    for (uint32_t t = tid; t < Mr * nb; t += GV_NT) {
+      uint32_t m = t / nb, kq = t - m * nb;
+      *(u32x4 *)(sX + m * KSM + 8 * kq) = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq);
+    }
+  } else {
+    const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+    for (uint32_t t = tid; t < Mr * ng; t += GV_NT) {
+      uint32_t m = t / ng, g = t - m * ng;
       float lo = 0.0f, hi = 0.0f;
 #pragma unroll
       for (int q = 0; q < UK / 8; q++) {
-        const u32x4 xv = x4[q];
+        u32x4 xv = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q));
         const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
         lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
         hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
+        if constexpr (WE == W_Q4) {
+          xv.y = as_u(b * r16);
+          xv.w = as_u(d * r16);
+        }
+        *(u32x4 *)(sX + m * KSM + g * UK + 8 * q) = xv;
       }
       if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
       else sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
-    }
-    __syncthreads();
-    if constexpr (WE == W_Q4) {
-      const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
-      for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
-        uint32_t m = t / nb, kq = t - m * nb;
-        u32x4 *px = (u32x4 *)(sX + m * KSM + 8 * kq);
-        u32x4 v = *px;
-        v.y = as_u(as_h2(v.y) * r16);
-        v.w = as_u(as_h2(v.w) * r16);
-        *px = v;
-      }
     }
   }
   __syncthreads();
