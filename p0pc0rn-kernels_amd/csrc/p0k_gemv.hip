@@ -293,7 +293,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 // minimum apply in registers. The weights are never dequantised: the MFMA multiplies the magic-biased codes, as in
 // the stream above, and the per-group corrections come from X' sums staged with X':
 //   q4: B holds 1024 + q (low nibbles) and 1024 + 16 q (high nibbles, in place), A holds x and x / 16 at those
-//       positions, so D = sum x q + G1 with G1 = 1024 X_lo + 64 X_hi; y += s (D - G1) + mn (X_lo + X_hi)
+//       positions, so D = sum x q + G1 with G1 = 1024 X_lo + 64 X_hi; y += s (D - G1) + mn (X_lo + X_hi), the MFMA
+//       starting from -G1
 //   q8: B holds 1152 + q; y += s (D - 1152 X)
 //   f16: B holds the weights; D accumulates across steps in the MFMA.
 // This is the fp32 arithmetic of the reference's CPU path (cpuGemm over fp32 dequantised weights) like the stream
@@ -398,9 +399,11 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       const f32x4 *gp = (const f32x4 *)(sG + unit * MT + 4 * kc);
       const f32x4 ga = gp[0], gb = gp[1];
       const float g1[4] = {ga.x, ga.z, gb.x, gb.z}, g2[4] = {ga.y, ga.w, gb.y, gb.w};
+      // the MFMA starts from -G1, so it returns D - G1 directly
+      const f32x4 ng1 = (f32x4){-g1[0], -g1[1], -g1[2], -g1[3]};
       f32x4 d[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) d[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = 0; i < 4; i++) d[i] = ng1;
       // q4: regroup the unit inside the wave: lane (kc, l16) takes word kc of row 16 i + l16 and that row's scale
       uint32_t qw[4], qs[4];
       if constexpr (WE == W_Q4) {
@@ -443,7 +446,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
           s = (float)__builtin_bit_cast(f16, (uint16_t)(rlo[i] ? (u.s[i] >> 16) : (u.s[i] & 0xffffu)));
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[i][r] = fmaf(s, d[i][r] - g1[r], fmaf(mn, g2[r], acc[i][r]));
+        for (int r = 0; r < 4; r++) acc[i][r] = fmaf(s, d[i][r], fmaf(mn, g2[r], acc[i][r]));
       }
     }
   };
