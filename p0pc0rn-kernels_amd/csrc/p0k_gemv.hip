@@ -125,11 +125,13 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   else woff = (r * p.wG + p.wk0 + kb0) * 2u;
   constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
 
+  const uint32_t sadj = 1024u - (r & 63u) * 12u;             // q4: code row -> scale word of row r in the record
   auto load = [&](Unit<WE> &u, uint32_t unit) {
-    const uint8_t *src = p.W + (woff + unit * USTRIDE);
+    const uint32_t o = woff + unit * USTRIDE;                  // 32-bit offsets from the uniform base: no 64-bit
+    const uint8_t *src = p.W + o;                              // address temporaries in the stream loop
     if constexpr (WE == W_Q4) {
       u.code = __builtin_nontemporal_load((const u32x4 *)src);
-      u.sm = __builtin_nontemporal_load((const uint32_t *)(src + 1024u - (r & 63u) * 12u));   // scale word r
+      u.sm = __builtin_nontemporal_load((const uint32_t *)(p.W + (o + sadj)));   // scale word r
     } else if constexpr (WE == W_Q8) {
 #pragma unroll
       for (int i = 0; i < 4; i++) u.code[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16u * i));
@@ -225,11 +227,14 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
     }
   };
 
-  // fill the ring before X' is staged, so HBM works while the prologue runs
+  // fill the ring before X' is staged, so HBM works while the prologue runs (unconditionally, clamped to the wave's
+  // last unit, in the refill order: the compiler then counts the loads in flight at the loop head exactly)
   Unit<WE> ring[PF];
 #pragma unroll
-  for (int j = 0; j < PF; j++)
-    if ((uint32_t)j < nuw) load(ring[j], u0 + j);
+  for (int j = 0; j < PF; j++) {
+    load(ring[j], u0 + ((uint32_t)j < nuw ? (uint32_t)j : nuw - 1u));
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // X' of the slice -> LDS in the pair order of the encoding; then per unit the X' sums over the low (even pair slot)
   // and high (odd pair slot) positions
@@ -269,6 +274,9 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
       // the old and the new slot contents apart and double the ring's registers
       const uint32_t nx = j0 + PF + j;
       load(ring[j], u0 + (nx < nuw ? nx : nuw - 1u));
+      // keep the refill here: left to itself the scheduler sinks all refills to the end of the batch behind one
+      // vmcnt(0), so a batch's loads would only start after the whole batch is reduced
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
