@@ -109,7 +109,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [MT][KSM / UK] (Xlo, Xhi) per unit
   float *sR = (float *)smem;                                   // after the stream: partials
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ch = wave / GV_KSUB, sub = wave % GV_KSUB;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
   const uint32_t nB = tile * 128u, kb0 = slice * KS;
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
     } else if constexpr (WE == W_Q8) {
 #pragma unroll
       for (int i = 0; i < 4; i++) u.code[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16u * i));
-      u.s = __builtin_nontemporal_load((const uint32_t *)(src + 4096u - (r & 63u) * 64u + (r & 62u) * 2u));
+      u.s = __builtin_nontemporal_load((const uint32_t *)(p.W + (o + 4096u - (r & 63u) * 64u + (r & 62u) * 2u)));
     } else {
 #pragma unroll
       for (int i = 0; i < 4; i++) u.v[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16 * i));
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [unit][MT] (G1, G2)
   float *sR = (float *)smem;                                   // after the stream: partials
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ch = wave / GV_KSUB, sub = wave % GV_KSUB, l16 = lane & 15, kc = lane >> 4;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
   const uint32_t nB = tile * 128u, kb0 = slice * KS;

@@ -87,7 +87,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    assert kern == ("gemv" if M == 1 else "gemv_mfma" if M <= 16 else "mfma_dma")
+    assert kern == ("gemv" if M == 1 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
@@ -120,10 +120,12 @@ def _adversarial_q8(rows, K, seed):
 
 @pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
 @pytest.mark.parametrize("path", ["gemv", "gemv_mfma", "mfma"])
-def test_dequant_bit_exact(dev, enc, path):
+def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
-    to exercise both decoder paths."""
+    to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream.)"""
+    if path == "gemv":
+        monkeypatch.setenv("P0K_GEMV_MF", "0")
     rows, K = 128, 256
     wb = _adversarial_q4(rows, K, 3) if enc.startswith("q4") else _adversarial_q8(rows, K, 4)
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
