@@ -135,17 +135,26 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
     }
 
     // ---- S^T for keys k0 .. k0+63: two 32-key blocks
+    // (the two key blocks' MFMA chains alternate, and each K fragment read is issued one MFMA ahead of its use)
     f32x16 sacc[2];
+    sacc[0] = (f32x16){};
+    sacc[1] = (f32x16){};
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-      sacc[kb] = (f32x16){};
-      const uint32_t key = 32 * kb + l32;
+    for (int s = 0; s < 8; s++)
 #pragma unroll
-      for (int s = 0; s < 8; s++) {
+      for (int kb = 0; kb < 2; kb++) {
+        const uint32_t key = 32 * kb + l32;
         const f16x8 a = *(const f16x8 *)(sK[b] + key * 128 + (((2 * s + gh) ^ (key & 15u)) * 8));
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[s], sacc[kb], 0, 0, 0);
       }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int q = 0; q < 14; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
     // ---- scores to the log2 domain: max over the raw scores (the scale is positive), then exp2(s * sl2 - m) with one
     //      FMA per score. Soft cap: s -> cap * tanh(s * scale / cap) first. Keys past the lane's limit are masked only
     //      in tiles that reach past some lane's limit (a wave-uniform test).
@@ -213,6 +222,14 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bp, oacc[db], 0, 0, 0);
       }
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+    for (int q = 0; q < 15; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
     if (t + 1 < ntile) lstore(b ^ 1);
     __builtin_amdgcn_s_waitcnt(0x0f70);                   // vmcnt(0): the next K tile has landed
     __syncthreads();
