@@ -34,8 +34,12 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
   __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ (((d >> 1) ^ (d >> 5)) & 15)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, gh = lane >> 5, l32 = lane & 31;
-  const uint32_t h = blockIdx.y, hk = h / (p.Hq / p.Hkv);
-  const uint32_t q0 = blockIdx.x * AT_BQ, qw = q0 + wave * 32 + l32;
+  // Workgroups go round-robin to the 8 XCDs; regroup them so each XCD walks whole heads (all query blocks of a head
+  // in a row): the head's K / V (Lk x 256 B) then stays in that XCD's L2 instead of being fetched once per query block
+  const uint32_t nqb = (p.Lq + AT_BQ - 1) / AT_BQ, nblk = nqb * p.Hq, b0 = blockIdx.x;
+  const uint32_t lin = (nblk & 7u) == 0u ? (b0 & 7u) * (nblk >> 3) + (b0 >> 3) : b0;
+  const uint32_t h = lin / nqb, hk = h / (p.Hq / p.Hkv);
+  const uint32_t q0 = (lin - h * nqb) * AT_BQ, qw = q0 + wave * 32 + l32;
   const uint32_t qc = qw < p.Lq ? qw : p.Lq - 1u;
 
   // this lane's query row: 8 steps of 16 d, lane half gh holds d = 16 s + 8 gh .. + 7
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
 
 hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
   if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
-  dim3 grid((p.Lq + AT_BQ - 1) / AT_BQ, p.Hq);
+  dim3 grid(((p.Lq + AT_BQ - 1) / AT_BQ) * p.Hq);
   if (p.cap > 0.0f) hipLaunchKernelGGL(k_attention<true>, grid, dim3(AT_NT), 0, s, p);
   else hipLaunchKernelGGL(k_attention<false>, grid, dim3(AT_NT), 0, s, p);
   return hipGetLastError();
