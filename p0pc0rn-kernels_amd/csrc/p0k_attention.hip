@@ -6,32 +6,35 @@
 //   i iff j <= min(i, nvalid - 1); 2: j < nvalid. Scores s = scale * q.k (scale defaults to 1/sqrt(128)), optionally
 //   soft-capped to cap * tanh(s / cap); O = softmax(s) V with an exact online softmax in fp32.
 //
-// One workgroup (4 waves) owns 128 queries of one head; each wave owns 32 of them and keeps its Q rows in registers.
-// Everything is computed transposed, so that a lane owns ONE query and the softmax statistics stay in the lane:
+// One workgroup owns 128 or 256 queries of one head (4 or 8 waves, 32 queries each; each wave keeps its Q rows in
+// registers). Everything is computed transposed, so that a lane owns ONE query and the softmax statistics stay in it:
 //   S^T (keys x queries) = K Q^T           v_mfma_f32_32x32x16_f16, A = K from LDS, B = Q^T from registers
 //   O^T (d x queries)   += V^T P           A = V^T from LDS, B = P = exp(S - m) from the S^T registers (fp16)
 // In the 32x32 layout lane l holds column l % 32 (its query) and 16 rows 8 (r/4) + 4 (l/32) + r%4, so a row maximum
 // or sum is a reduction over the lane's registers plus one exchange with lane l ^ 32. The 16 keys a lane contributes
-// to one P.V step are exactly the keys its S^T registers hold, so P never leaves the registers; V is staged in LDS
-// transposed ([d][key]) so those keys are two 8-byte reads. Keys come in tiles of 64 through double-buffered LDS (the
-// next tile's global loads are issued before this tile's MFMAs); both LDS tiles are XOR-swizzled so the 16-byte K reads
-// and the 8-byte V reads of a wave hit distinct banks (the V swizzle also folds in d >> 5, so the rows d and d + 32 that
-// one read instruction pairs land in different banks). K arrives by the load-to-LDS path; V is transposed through
-// registers. Two waves per SIMD (256 registers each) let one wave's softmax run under the other's MFMAs.
+// to one P.V step are exactly the keys its S^T registers hold, so P never leaves the registers. Keys come in tiles of
+// 64 through a two-stage LDS ring (the next tile's loads are issued before this tile's MFMAs); K and V both arrive
+// by the load-to-LDS path in their HBM layout [key][d], and the V^T operand is read with the transposing
+// ds_read_b64_tr_b16 (four keys of one d per lane). Both tiles are XOR-swizzled so the 16-byte K reads and the
+// transposed V reads of a wave hit distinct banks. Two waves per SIMD (256 registers each) let one wave's softmax
+// run under the other's MFMAs; with 256 queries a K / V tile is fetched into LDS once per 256 queries instead of 128.
 #include "p0k_device.h"
 #include "p0k_launch.h"
+#include <cstdlib>
 
 namespace p0k {
 
-#ifndef P0K_AT_BQ
-#define P0K_AT_BQ 128
+#ifndef P0K_AT_S
+#define P0K_AT_S 2
 #endif
-constexpr int AT_BQ = P0K_AT_BQ, AT_BK = 64, AT_NT = 2 * AT_BQ, AT_NW = AT_NT / 64;   // 32 queries per wave
+constexpr int AT_S = P0K_AT_S, AT_BK = 64;
 
-template <bool CAP>
-__global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) f16 sK[2][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ (key & 15)
-  __shared__ __attribute__((aligned(16))) f16 sV[2][128 * AT_BK];   // [d][key], 4-key unit u at u ^ (((d >> 1) ^ (d >> 5)) & 15)
+// AT_BQ queries per workgroup (128 or 256), 32 per wave
+template <int AT_BQ, bool CAP>
+__global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(AttnParams p) {
+  constexpr int AT_NT = 2 * AT_BQ, AT_NW = AT_NT / 64;
+  __shared__ __attribute__((aligned(16))) f16 sK[AT_S][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ (key & 15)
+  __shared__ __attribute__((aligned(16))) f16 sV[AT_S][AT_BK * 128];   // [key][d], 16-byte chunk c at c ^ 4 (key & 3)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, gh = lane >> 5, l32 = lane & 31;
   // Workgroups go round-robin to the 8 XCDs; regroup them so each XCD walks whole heads (all query blocks of a head
@@ -64,12 +67,9 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
   const float sl2 = p.scale * 1.4426950408889634f;
 
   const uint16_t *Kb = p.K + (size_t)hk * p.Lk * 128, *Vb = p.V + (size_t)hk * p.Lk * 128;
-  // V staging: thread (vkg, vdc, vh) holds keys 4 vkg + VPT vh .. + VPT-1 of d 8 vdc .. + 7
-  constexpr int VPT = 4 * 256 / AT_NT;                   // keys per thread
-  u32x4 vr[VPT];
-  const uint32_t vkg = tid & 15, vdc = (tid >> 4) & 15, vh = tid >> 8;
-  // K goes global -> LDS by the load-to-LDS path: instruction i of wave w fills keys 4 (4 i + w) .. + 3 (1 KB), lane l
-  // the 16-byte slot l % 16 of key l / 16, i.e. logical chunk (l % 16) ^ (key & 15)
+  // K and V go global -> LDS by the load-to-LDS path: instruction i of wave w fills keys 4 (NW i + w) .. + 3 (1 KB),
+  // lane l the 16-byte slot l % 16 of key l / 16, i.e. logical chunk (l % 16) ^ (key & 15) of K, (l % 16) ^ 4 (key & 3)
+  // of V
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t sk0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)&sK[0][0];
   auto kdma = [&](uint32_t t, int b) {
@@ -82,60 +82,44 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
       asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(Kb) : "memory");
     }
   };
-  auto gload = [&](uint32_t t) {
+  const uint32_t sv0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)&sV[0][0];
+  auto vdma = [&](uint32_t t, int b) {
     const uint32_t k0 = t * AT_BK;
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-      const uint32_t vk = k0 + 4 * vkg + VPT * vh + i;
-      vr[i] = *(const u32x4 *)(Vb + (size_t)(vk < p.Lk ? vk : p.Lk - 1u) * 128 + vdc * 8);
+    for (int i = 0; i < 16 / AT_NW; i++) {
+      const uint32_t kr = 4 * (AT_NW * i + wv) + lane / 16, key = k0 + kr, c = (lane & 15) ^ (4 * (kr & 3));
+      const uint32_t off = ((key < p.Lk ? key : p.Lk - 1u) * 128 + c * 8) * 2;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(sv0 + (uint32_t)(b * AT_BK * 128 + 4 * (AT_NW * i + wv) * 128) * 2);
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(off), "s"(Vb) : "memory");
     }
   };
-  auto lstore = [&](int b) {
-    if constexpr (VPT == 4) {
-      // The 16 threads of one d cover the 16 units of its row (half the banks), so the two d a 32-lane half writes
-      // per instruction must differ in parity (row parity picks the bank half): odd 16-lane groups write the rows
-      // of each pair (2w, 2w+1) in swapped order, picking the halves with a lane-dependent v_perm selector.
-      const uint32_t odd = (tid >> 4) & 1u;
-      const uint32_t s0 = odd ? 0x07060302u : 0x05040100u, s1 = odd ? 0x05040100u : 0x07060302u;
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-        const uint32_t a0 = vr[0][w], a1 = vr[1][w], a2 = vr[2][w], a3 = vr[3][w];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const uint32_t sel = h ? s1 : s0, d = vdc * 8 + 2 * w + (h ^ odd);
-          *(u32x2 *)(sV[b] + d * AT_BK + ((vkg ^ (((d >> 1) ^ (d >> 5)) & 15u)) * 4)) = (u32x2){perm(a1, a0, sel), perm(a3, a2, sel)};
-        }
-      }
-    } else {                                               // two keys per thread: half of a 4-key unit
-      const uint16_t *v0 = (const uint16_t *)&vr[0], *v1 = (const uint16_t *)&vr[1];
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const uint32_t d = vdc * 8 + j;
-        *(uint32_t *)(sV[b] + d * AT_BK + ((vkg ^ (((d >> 1) ^ (d >> 5)) & 15u)) * 4) + 2 * vh) =
-            (uint32_t)v0[j] | ((uint32_t)v1[j] << 16);
-      }
-    }
-  };
-
-
   f32x16 oacc[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) oacc[i] = (f32x16){};
   float m = -1.0e30f, l = 0.0f;
 
-  if (ntile) {
-    kdma(0, 0);
-    gload(0);
-    lstore(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0x0f70);                     // vmcnt(0): this wave's K rows have landed
+  // AT_S-stage ring: tile t lives in buffer t % AT_S; tile t + AT_S - 1 is issued at the top of tile t into the buffer
+  // every wave left at the barrier that ended tile t - 1. A wave's own loads complete in order, so waiting until at
+  // most (AT_S - 2) tiles' worth of them are outstanding means its share of the next tile has landed.
+  constexpr int PER = 32 / AT_NW;                           // load instructions per wave per tile (K and V)
+  constexpr int NOUT = (AT_S - 2) * PER;
+  constexpr int WAIT_RING = (NOUT & 15) | ((NOUT >> 4) << 14) | 0x0f70;
+#pragma unroll
+  for (int i = 0; i < AT_S - 1; i++)
+    if ((uint32_t)i < ntile) {
+      kdma(i, i);
+      vdma(i, i);
+    }
+  if (ntile >= (uint32_t)(AT_S - 1)) __builtin_amdgcn_s_waitcnt(WAIT_RING);
+  else __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
+  int b = 0;
   for (uint32_t t = 0; t < ntile; t++) {
-    const int b = t & 1;
     const uint32_t k0 = t * AT_BK;
-    if (t + 1 < ntile) {
-      gload(t + 1);
-      kdma(t + 1, b ^ 1);                                   // the other K buffer: every wave left it at the last barrier
+    if (t + AT_S - 1 < ntile) {
+      const int bn = b == 0 ? AT_S - 1 : b - 1;
+      kdma(t + AT_S - 1, bn);
+      vdma(t + AT_S - 1, bn);
     }
 
     // ---- S^T for keys k0 .. k0+63: two 32-key blocks
@@ -216,13 +200,16 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
       const f16x8 bp = {(f16)sacc[kb][8 * h2 + 0], (f16)sacc[kb][8 * h2 + 1], (f16)sacc[kb][8 * h2 + 2],
                         (f16)sacc[kb][8 * h2 + 3], (f16)sacc[kb][8 * h2 + 4], (f16)sacc[kb][8 * h2 + 5],
                         (f16)sacc[kb][8 * h2 + 6], (f16)sacc[kb][8 * h2 + 7]};
-      const uint32_t u1 = 8 * kb + 4 * h2 + gh, u2 = u1 + 2;   // 4-key units of the lane's 8 keys
 #pragma unroll
       for (int db = 0; db < 4; db++) {
-        const uint32_t d = 32 * db + l32, sw = ((d >> 1) ^ (d >> 5)) & 15u;
-        const u32x2 lo = *(const u32x2 *)(sV[b] + d * AT_BK + ((u1 ^ sw) * 4));
-        const u32x2 hi = *(const u32x2 *)(sV[b] + d * AT_BK + ((u2 ^ sw) * 4));
-        const f16x8 av = __builtin_bit_cast(f16x8, (u32x4){lo.x, lo.y, hi.x, hi.y});
+        // transposed read: lane 4 j + a of each 16-lane group addresses key j, d 4 a .. 4 a + 3; lane 4 a + b then
+        // receives d 4 a + b of keys j = 0..3. Lanes 16..31 of a half take the next 16 d; half gh the keys 4 gh ..
+        const uint32_t kr = 32 * kb + 16 * h2 + 4 * gh + ((lane >> 2) & 3), c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane >> 1) & 1);
+        const f16 *va = sV[b] + kr * 128 + ((c ^ (4 * (kr & 3))) * 8) + 4 * (lane & 1);
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)va);
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(va + 8 * 128));
+        const f16x8 av = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bp, oacc[db], 0, 0, 0);
       }
     }
@@ -234,9 +221,10 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < ntile) lstore(b ^ 1);
-    __builtin_amdgcn_s_waitcnt(0x0f70);                   // vmcnt(0): the next K tile has landed
+    if (t + AT_S - 1 < ntile) __builtin_amdgcn_s_waitcnt(WAIT_RING);   // this wave's share of tile t + 1 has landed
+    else __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
+    b = b == AT_S - 1 ? 0 : b + 1;
   }
 
   // ---- O = O^T / l: lane writes its query's 128 values in runs of 4 d
@@ -255,11 +243,26 @@ __global__ __launch_bounds__(AT_NT, 2 * 256 / AT_NT) void k_attention(AttnParams
   }
 }
 
-hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
+int attention_bq(uint32_t Lq, uint32_t Hq, int cus) {
+  if (const char *ov = getenv("P0K_ATTN_BQ")) {                 // tuning / tests: force 128 or 256
+    const int v = atoi(ov);
+    if (v == 128 || v == 256) return v;
+  }
+  // 256 queries share each K / V tile (half the LDS fill per query) once that still gives every CU a workgroup
+  return (uint64_t)((Lq + 255) / 256) * Hq >= (uint64_t)cus ? 256 : 128;
+}
+
+hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s) {
   if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
-  dim3 grid(((p.Lq + AT_BQ - 1) / AT_BQ) * p.Hq);
-  if (p.cap > 0.0f) hipLaunchKernelGGL(k_attention<true>, grid, dim3(AT_NT), 0, s, p);
-  else hipLaunchKernelGGL(k_attention<false>, grid, dim3(AT_NT), 0, s, p);
+  const int bq = attention_bq(p.Lq, p.Hq, cus);
+  dim3 grid(((p.Lq + bq - 1) / bq) * p.Hq);
+  if (bq == 256) {
+    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<256, true>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((k_attention<256, false>), grid, dim3(512), 0, s, p);
+  } else {
+    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<128, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((k_attention<128, false>), grid, dim3(256), 0, s, p);
+  }
   return hipGetLastError();
 }
 

@@ -34,7 +34,8 @@ struct AttnParams {
   uint32_t Lq, Lk, ldo, Hq, Hkv, mode, nvalid;
   float scale, cap;            // natural-log scale; cap > 0: scores -> cap * tanh(scores / cap)
 };
-hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+int attention_bq(uint32_t Lq, uint32_t Hq, int cus);   // queries per workgroup
+hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s);
 // pixstats and GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109)
 hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, float *r, hipStream_t s);
 hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);

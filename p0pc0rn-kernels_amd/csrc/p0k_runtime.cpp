@@ -459,7 +459,7 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
       (r = check_live(c, a->v_buf, a->v_size, "attention", "v")) || (r = check_live(c, a->o_buf, a->o_size, "attention", "o")))
     return r;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_attention(p, c->stream);
+  hipError_t e = p0k::launch_attention(p, p0k::MI355X_CUS, c->stream);
   if (e != hipSuccess) return hip_err(e, "attention launch");
   return P0K_OK;
 }

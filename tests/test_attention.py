@@ -85,9 +85,12 @@ def cos_and_err(got, want):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bq", [128, 256])
 @pytest.mark.parametrize("c", ATT + MORE, ids=lambda c: c["label"])
-def test_attention_matches_oracle(dev, c):
-    print(f"attention {c}", flush=True)
+def test_attention_matches_oracle(dev, c, bq, monkeypatch):
+    """Both workgroup sizes (128 / 256 queries) on every case; the library picks 256 only for large grids."""
+    monkeypatch.setenv("P0K_ATTN_BQ", str(bq))
+    print(f"attention bq={bq} {c}", flush=True)
     q, k, v = setup(c, 21, 1.0 if c.get("cap") else 0.5)
     Lq, Hq = c["Lq"], c["Hq"]
     ld = Hq * 128 + (8 if c["mode"] == 2 else 0)                       # a padded O row for one case
