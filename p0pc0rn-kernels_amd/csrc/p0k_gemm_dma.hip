@@ -3,8 +3,9 @@
 // M0 + 16 lane / 4 lane, no registers, no LDS store instructions), weights are decoded in registers right before the
 // matrix core uses them.
 //
-// One workgroup (4 waves, 2 x 2) computes a TBM x TBN tile (TBM, TBN in {128, 256}); a wave owns (TBM/2) x (TBN/2)
-// as 32x32 v_mfma_f32_32x32x16_f16 blocks. K moves in steps of 64 through a ring of S LDS stages:
+// One workgroup computes a TBM x TBN tile (TBM, TBN in {128, 256}): 4 waves (2 x 2) for the smaller tiles, 8 waves
+// (2 x 4, two per SIMD, so one wave's decode and LDS reads run under the other's MFMAs) for 256 x 256; a wave owns
+// (TBM/2) x (TBN/2) or 128 x 64 as 32x32 v_mfma_f32_32x32x16_f16 blocks. K moves in steps of 64 through a ring of S LDS stages:
 //   X' rows      [row][128 B], the 16-byte chunk c of row r at c ^ ((r >> 1) & 7)
 //   f16 weights  the same layout, one row per ws column
 //   q4 records   per 64-column block and 32-k record: the 64 code rows [col][16 B] as stored, and the 64 (scale, min)
@@ -30,30 +31,36 @@ namespace p0k {
 
 namespace {
 
-constexpr int DBK = 64, DNT = 256, DLDC = 128 + 4;
+constexpr int DBK = 64, DLDC = 128 + 4;
 
-template <int WE, int TBM, int TBN>
+// NWV waves (4: 2 x 2, or 8: 2 x 4 with two waves per SIMD; 8 only for 256 x 256)
+template <int WE, int TBM, int TBN, int NWV = 4>
 struct DT {
+  static constexpr int NT = 64 * NWV;
   static constexpr int NBLK = TBN / 64;                                        // 64-column weight blocks
+  // DMA instructions per stage, in groups of NWV (one per wave): X' row blocks (8 rows), weight code blocks, then
+  // weight scale words (q8: padded to NWV with repeats of the last block's)
+  static constexpr int NIA = TBM / 8;
+  static constexpr int NIC = WE == W_F16 ? TBN / 8 : (WE == W_Q4 ? NBLK * 2 : NBLK * 4);
+  static constexpr int NIS = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 : NWV);
+  static_assert(NIA % NWV == 0 && NIC % NWV == 0 && NIS % NWV == 0, "DMA instructions per wave");
+  static constexpr int NW = (NIA + NIC + NIS) / NWV;                           // per wave
+  static constexpr int WA = NIA / NWV, WC = NIC / NWV;
   static constexpr int A_BYTES = TBM * 128;
   static constexpr int BC_BYTES = WE == W_F16 ? TBN * 128 : (WE == W_Q4 ? NBLK * 2 * 1024 : NBLK * 4 * 1024);
-  static constexpr int BS_BYTES = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 * 256 : 4 * 256);   // q8: NBLK or pad
+  static constexpr int BS_BYTES = NIS * 256;
   static constexpr int STAGE = A_BYTES + BC_BYTES + BS_BYTES;
-  static constexpr bool TWO = 4 * STAGE <= 160 * 1024 && TBM * TBN < 256 * 256;  // two workgroups per CU
+  static constexpr bool TWO = NWV == 4 && 4 * STAGE <= 160 * 1024 && TBM * TBN < 256 * 256;  // two workgroups per CU
   static constexpr int BUDGET = TWO ? 80 * 1024 : 160 * 1024;
   static constexpr int S = 3 * STAGE <= BUDGET ? 3 : 2;
   static constexpr int SMEM_C = 128 * DLDC * 4;
   static constexpr int SMEM = S * STAGE > SMEM_C ? S * STAGE : SMEM_C;
   static_assert(SMEM <= BUDGET, "LDS budget");
-  // DMA instructions per stage, in groups of four (one per wave): X' row blocks (8 rows), weight code blocks, then
-  // weight scale words (q8: padded to 4 with repeats of the last block's)
-  static constexpr int NIA = TBM / 8;
-  static constexpr int NIC = WE == W_F16 ? TBN / 8 : (WE == W_Q4 ? NBLK * 2 : NBLK * 4);
-  static constexpr int NIS = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 : 4);
-  static constexpr int NW = (NIA + NIC + NIS) / 4;                             // per wave
-  static constexpr int WA = NIA / 4, WC = NIC / 4;
-  static constexpr int BI = TBM / 64, BJ = TBN / 64;                           // 32x32 blocks per wave
-  static constexpr int OCC = TWO ? 2 : 1;
+  static constexpr int WGN = NWV / 2;                                          // waves along N
+  static constexpr int WTM = TBM / 2, WTN = TBN / WGN;                         // a wave's sub-tile
+  static constexpr int BI = WTM / 32, BJ = WTN / 32;                           // 32x32 blocks per wave
+  static constexpr int WGS = TWO ? 2 : 1;                                      // workgroups per CU
+  static constexpr int OCC = WGS * NWV / 4;                                    // waves per SIMD
 };
 
 __device__ __forceinline__ uint32_t lds_u32(const void *p) {
@@ -145,12 +152,12 @@ __device__ __forceinline__ void tile_order(const Params &p, uint32_t bid, uint32
 }
 
 // XG: X' rows (X_F16: an fp16 matrix) or the conv3 gather (X_CONV3: input voxels [vox][Ci], padding taps read Z)
-template <int WE, int XG, int TBM, int TBN>
-__global__ __launch_bounds__(DNT, (DT<WE, TBM, TBN>::OCC))
-__attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::OCC)))) void k_gemm_dma(Params p) {
-  using T = DT<WE, TBM, TBN>;
+template <int WE, int XG, int TBM, int TBN, int NWV>
+__global__ __launch_bounds__((64 * NWV))
+__attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV>::OCC), (DT<WE, TBM, TBN, NWV>::OCC)))) void k_gemm_dma(Params p) {
+  using T = DT<WE, TBM, TBN, NWV>;
   constexpr int S = T::S, BI = T::BI, BJ = T::BJ, NW = T::NW;
-  constexpr int WTM = TBM / 2, WTN = TBN / 2;
+  constexpr int WTM = T::WTM, WTN = T::WTN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[T::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -160,13 +167,13 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   const uint32_t nk = p.K / DBK;
 
   // ---- per-lane DMA sources (step 0) and per-step advances; instruction t of this wave is number 4 t + wave of
-  //      the stage's list
+  //      the stage's list (NWV t + wave)
   uint32_t src[NW];                                   // byte offsets from X' / the weights (both < 4 GiB)
   uint32_t cv_it[XG == X_CONV3 ? T::WA : 1], cv_yx[XG == X_CONV3 ? T::WA : 1];   // conv3 row contexts
   uint32_t dst[NW];                                   // byte offset inside a stage
 #pragma unroll
   for (int t = 0; t < NW; t++) {
-    const int q = 4 * t + wave;
+    const int q = NWV * t + wave;
     if (t < T::WA) {                                  // X' rows 8q .. 8q+7
       const uint32_t r = 8 * q + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
       uint32_t m = mB + r;
@@ -190,7 +197,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       }
       dst[t] = q * 1024;
     } else if (t < T::WA + T::WC) {
-      const int b = q - 4 * T::WA;
+      const int b = q - NWV * T::WA;
       if constexpr (WE == W_F16) {                    // weight rows of ws columns 8b .. 8b+7
         const uint32_t r = 8 * b + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
         src[t] = (wrow(p, nB + r) * p.wG + p.wk0 + 8 * c) * 2u;
@@ -203,7 +210,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
       }
       dst[t] = T::A_BYTES + b * 1024;
     } else {
-      const int b = q - 4 * (T::WA + T::WC);
+      const int b = q - NWV * (T::WA + T::WC);
       if constexpr (WE == W_Q4) {                     // (scale, min) word of block b / 2, record b & 1
         const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
         src[t] = ((r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + 1024u + (r & 63u) * 4u;
@@ -246,7 +253,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
   };
 
   // ---- fragments
-  const int wm = wave >> 1, wn = wave & 1, l32 = lane & 31, hh = lane >> 5, sw = (l32 >> 1) & 7;
+  const int wm = wave / T::WGN, wn = wave % T::WGN, l32 = lane & 31, hh = lane >> 5, sw = (l32 >> 1) & 7;
   const int rdA = (wm * WTM + l32) * 128;              // byte offset of the lane's first A row in a stage
   f32x16 acc[BI][BJ];
 #pragma unroll
@@ -438,23 +445,23 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN>::OCC), (DT<WE, TBM, TBN>::O
             }
       }
       __syncthreads();
-      epilogue<DNT>(p, sC, DLDC, 128, mB + v * 128, nB + h * 128, tid);
+      epilogue<T::NT>(p, sC, DLDC, 128, mB + v * 128, nB + h * 128, tid);
       if (v + 1 < TBM / 128 || h + 1 < TBN / 128) __syncthreads();
     }
 }
 
-template <int WE, int XG, int TBM, int TBN>
+template <int WE, int XG, int TBM, int TBN, int NWV = 4>
 hipError_t launch_dma_one(const Params &p, hipStream_t s) {
   Params q = p;
   q.tilesM = (p.M + TBM - 1) / TBM;
   q.tilesN = (p.N + TBN - 1) / TBN;
-  hipLaunchKernelGGL((k_gemm_dma<WE, XG, TBM, TBN>), dim3(q.tilesM * q.tilesN), dim3(DNT), 0, s, q);
+  hipLaunchKernelGGL((k_gemm_dma<WE, XG, TBM, TBN, NWV>), dim3(q.tilesM * q.tilesN), dim3(64 * NWV), 0, s, q);
   return hipGetLastError();
 }
 
 template <int WE, int XG>
 hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
-  if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256>(p, s);
+  if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256, 8>(p, s);
   if (bm == 256 && bn == 128) return launch_dma_one<WE, XG, 256, 128>(p, s);
   if (bm == 128 && bn == 256) return launch_dma_one<WE, XG, 128, 256>(p, s);
   if (bm == 128 && bn == 128) return launch_dma_one<WE, XG, 128, 128>(p, s);
@@ -530,16 +537,17 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn) {
   auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
     if (m == 256 && n == 256) return 1;
-    if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::OCC) : (DT<W_F16, 128, 256>::OCC);
-    if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::OCC : (m == 128 ? DT<W_Q4, 128, 256>::OCC : DT<W_Q4, 256, 128>::OCC);
-    return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::OCC : (m == 128 ? DT<W_Q8, 128, 256>::OCC : DT<W_Q8, 256, 128>::OCC);
+    if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
+    if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
+    return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
   };
-  // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: the quantised weights
-  // favour 256-row tiles (each decoded weight feeds four 32-row blocks instead of two)
+  // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: 256 x 256 runs 8 waves
+  // (two per SIMD), the others 4; the quantised weights favour 256-row tiles (each decoded weight feeds four 32-row
+  // blocks instead of two)
   struct C { unsigned m, n; double rate; };
-  const C c16[] = {{256, 256, 1.0}, {128, 256, 0.96}, {256, 128, 0.98}, {128, 128, 0.93}};
-  const C cq4[] = {{256, 256, 0.91}, {128, 256, 0.74}, {256, 128, 1.0}, {128, 128, 0.75}};
-  const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.83}, {256, 128, 0.92}, {128, 128, 0.86}};
+  const C c16[] = {{256, 256, 1.0}, {128, 256, 0.94}, {256, 128, 0.92}, {128, 128, 0.91}};
+  const C cq4[] = {{256, 256, 1.0}, {128, 256, 0.68}, {256, 128, 0.91}, {128, 128, 0.68}};
+  const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.75}, {256, 128, 0.78}, {128, 128, 0.78}};
   // the conv3 gather computes each row's tap address per step: two workgroups of 128 x 128 per CU hide it best
   // (f16 weights, 13 x 92 x 160 x 128 clip: 128 x 128 252 us, 256 x 128 272, 256 x 256 382, 128 x 256 409)
   const C cg[] = {{256, 256, 0.66}, {128, 256, 0.62}, {256, 128, 0.93}, {128, 128, 1.0}};
