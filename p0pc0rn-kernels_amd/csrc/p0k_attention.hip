@@ -21,7 +21,6 @@
 #include "p0k_device.h"
 #include "p0k_launch.h"
 #include <cstdlib>
-#include <cstring>
 
 namespace p0k {
 
@@ -40,26 +39,8 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, gh = lane >> 5, l32 = lane & 31;
   // Workgroups go round-robin to the 8 XCDs; regroup them so each XCD walks whole heads (all query blocks of a head
   // in a row): the head's K / V (Lk x 256 B) then stays in that XCD's L2 instead of being fetched once per query block
-  // (the whole blocks [0, t0) that way; the key-split items after them likewise per XCD, both halves of a block on
-  // one XCD)
-  const uint32_t nqb = (p.Lq + AT_BQ - 1) / AT_BQ, b0 = blockIdx.x;
-  uint32_t lin, half = 0;
-  const bool split = b0 >= p.t0;
-  if (!split) {
-    lin = (p.t0 & 7u) == 0u ? (b0 & 7u) * (p.t0 >> 3) + (b0 >> 3) : b0;
-  } else {
-    const uint32_t j = b0 - p.t0;
-    uint32_t g;
-    if ((p.nsplit & 7u) == 0u) {
-      const uint32_t r = j >> 3;
-      g = (j & 7u) * (p.nsplit >> 3) + (r >> 1);
-      half = r & 1u;
-    } else {
-      g = j >> 1;
-      half = j & 1u;
-    }
-    lin = p.t0 + g;
-  }
+  const uint32_t nqb = (p.Lq + AT_BQ - 1) / AT_BQ, nblk = nqb * p.Hq, b0 = blockIdx.x;
+  const uint32_t lin = (nblk & 7u) == 0u ? (b0 & 7u) * (nblk >> 3) + (b0 >> 3) : b0;
   const uint32_t h = lin / nqb, hk = h / (p.Hq / p.Hkv);
   const uint32_t q0 = (lin - h * nqb) * AT_BQ, qw = q0 + wave * 32 + l32;
   const uint32_t qc = qw < p.Lq ? qw : p.Lq - 1u;
@@ -82,9 +63,7 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
   if (p.mode == 1) qlim = (qc < p.nvalid - 1 ? qc : p.nvalid - 1) + 1;
   else if (p.mode == 2) qlim = p.nvalid;
   qlim = qlim < p.Lk ? qlim : p.Lk;
-  const uint32_t ntk = (kend + AT_BK - 1) / AT_BK;
-  // the key tiles of this item: all, or one half
-  const uint32_t ts = split && half ? ntk / 2 : 0u, te = split && !half ? ntk / 2 : ntk;
+  const uint32_t ntile = (kend + AT_BK - 1) / AT_BK;
   const float sl2 = p.scale * 1.4426950408889634f;
 
   const uint16_t *Kb = p.K + (size_t)hk * p.Lk * 128, *Vb = p.V + (size_t)hk * p.Lk * 128;
@@ -127,17 +106,17 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
   constexpr int WAIT_RING = (NOUT & 15) | ((NOUT >> 4) << 14) | 0x0f70;
 #pragma unroll
   for (int i = 0; i < AT_S - 1; i++)
-    if (ts + i < te) {
-      kdma(ts + i, i);
-      vdma(ts + i, i);
+    if ((uint32_t)i < ntile) {
+      kdma(i, i);
+      vdma(i, i);
     }
-  if (te - ts >= (uint32_t)(AT_S - 1)) __builtin_amdgcn_s_waitcnt(WAIT_RING);
+  if (ntile >= (uint32_t)(AT_S - 1)) __builtin_amdgcn_s_waitcnt(WAIT_RING);
   else __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
   int b = 0;
-  for (uint32_t t = ts; t < te; t++) {
+  for (uint32_t t = 0; t < ntile; t++) {
     const uint32_t k0 = t * AT_BK;
-    if (t + AT_S - 1 < te) {
+    if (t + AT_S - 1 < ntile) {
       const int bn = b == 0 ? AT_S - 1 : b - 1;
       kdma(t + AT_S - 1, bn);
       vdma(t + AT_S - 1, bn);
@@ -242,51 +221,10 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
     __builtin_amdgcn_sched_barrier(0);
-    if (t + AT_S - 1 < te) __builtin_amdgcn_s_waitcnt(WAIT_RING);      // this wave's share of tile t + 1 has landed
+    if (t + AT_S - 1 < ntile) __builtin_amdgcn_s_waitcnt(WAIT_RING);   // this wave's share of tile t + 1 has landed
     else __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
     b = b == AT_S - 1 ? 0 : b + 1;
-  }
-
-  if (split) {
-    // this half's state -> the workspace as [value][thread] (O^T registers, then m and l): plain stores, then one
-    // agent-scope acquire-release counter update per half (writes them back from this XCD's L2; for the second half
-    // to arrive, invalidates its caches before it reads the first's)
-    __shared__ uint32_t sLast;
-    constexpr uint32_t PV = 66 * AT_NT;                          // floats per half
-    float *pw = p.part + (size_t)(lin - p.t0) * 2 * PV + tid;
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) pw[half * PV + (16 * db + r) * AT_NT] = oacc[db][r];
-    pw[half * PV + 64 * AT_NT] = m;
-    pw[half * PV + 65 * AT_NT] = l;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(p.cnt + (lin - p.t0), 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      sLast = old == 1u ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!sLast) return;
-    // merge in a fixed order (half 0, then half 1), whichever arrives last: m = max(m0, m1), O = O0 2^(m0-m) +
-    // O1 2^(m1-m), l likewise (m is in the log2 domain; -1e30 = no visible key yet)
-    const float *po = pw + (half ^ 1u) * PV;
-    const float mo = po[64 * AT_NT], lo = po[65 * AT_NT];
-    const float m0 = half ? mo : m, m1 = half ? m : mo;
-    const float mx = fmaxf(m0, m1);
-    const float a0 = __builtin_amdgcn_exp2f(m0 - mx), a1 = __builtin_amdgcn_exp2f(m1 - mx);
-    // x0 a0 rounded, then one FMA with x1 a1: the same operations whichever half this is
-    l = half ? fmaf(l, a1, lo * a0) : fmaf(lo, a1, l * a0);
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float own = oacc[db][r], oth = po[(16 * db + r) * AT_NT];
-        const float x0 = half ? oth : own, x1 = half ? own : oth;
-        oacc[db][r] = fmaf(x1, a1, x0 * a0);
-      }
-    if (tid == 0) __hip_atomic_store(p.cnt + (lin - p.t0), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- O = O^T / l: lane writes its query's 128 values in runs of 4 d
@@ -314,48 +252,16 @@ int attention_bq(uint32_t Lq, uint32_t Hq, int cus) {
   return (uint64_t)((Lq + 255) / 256) * Hq >= (uint64_t)cus ? 256 : 128;
 }
 
-// Key split: when the last round of query blocks would leave at least half of the workgroup slots empty (384
-// blocks of 256 queries on 256 CUs: 1.5 rounds), those blocks run as two halves of their key range, so the last round
-// is full and half as long. A head's K / V stays in L2 across its blocks, so the halves stay compute-bound; each
-// half's O^T, m and l go through the workspace (66 floats per thread) and the half that arrives second merges them.
-// Only with at least 16 key tiles (a half of >= 512 keys). P0K_ATTN_SPLIT=0 turns it off, =all splits every block
-// (tests).
-void attention_split(const AttnParams &p, int cus, uint32_t *t0, uint32_t *nsplit) {
-  const int bq = attention_bq(p.Lq, p.Hq, cus);
-  const uint32_t nblk = (p.Lq + bq - 1) / bq * p.Hq, slots = (uint32_t)cus * (bq == 256 ? 1u : 2u);
-  *t0 = nblk;
-  *nsplit = 0;
-  const char *ov = getenv("P0K_ATTN_SPLIT");
-  if (ov && strcmp(ov, "0") == 0) return;
-  if (ov && strcmp(ov, "all") == 0) {
-    *t0 = 0;
-    *nsplit = nblk;
-    return;
-  }
-  const uint32_t tail = nblk % slots;
-  if (tail == 0 || 2 * tail > slots || (p.Lk + 63) / 64 < 16) return;
-  *t0 = nblk - tail;
-  *nsplit = tail;
-}
-
-uint64_t attention_part_bytes(const AttnParams &p, int cus, uint32_t nsplit) {
-  return (uint64_t)nsplit * 2 * 66 * (2 * attention_bq(p.Lq, p.Hq, cus)) * sizeof(float);
-}
-
 hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s) {
   if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
   const int bq = attention_bq(p.Lq, p.Hq, cus);
-  const uint32_t nblk = (p.Lq + bq - 1) / bq * p.Hq;
-  AttnParams q = p;
-  if (q.nsplit == 0) q.t0 = nblk;                                  // no split
-  else if (q.t0 + q.nsplit != nblk || !q.part || !q.cnt) return hipErrorInvalidValue;
-  dim3 grid(q.t0 + 2 * q.nsplit);
+  dim3 grid(((p.Lq + bq - 1) / bq) * p.Hq);
   if (bq == 256) {
-    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<256, true>), grid, dim3(512), 0, s, q);
-    else hipLaunchKernelGGL((k_attention<256, false>), grid, dim3(512), 0, s, q);
+    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<256, true>), grid, dim3(512), 0, s, p);
+    else hipLaunchKernelGGL((k_attention<256, false>), grid, dim3(512), 0, s, p);
   } else {
-    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<128, true>), grid, dim3(256), 0, s, q);
-    else hipLaunchKernelGGL((k_attention<128, false>), grid, dim3(256), 0, s, q);
+    if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<128, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((k_attention<128, false>), grid, dim3(256), 0, s, p);
   }
   return hipGetLastError();
 }

@@ -312,7 +312,6 @@ int prepare_attention(const p0k_attn_args *a, AttnParams *out, std::string *err)
     out->Lq = Lq; out->Lk = Lk; out->ldo = ldo; out->Hq = Hq; out->Hkv = Hkv; out->mode = a->mode; out->nvalid = nvalid;
     out->scale = a->scale != 0.0f ? a->scale : 0.08838834764831845f;   // 1 / sqrt(128)
     out->cap = a->cap;
-    out->t0 = 0; out->nsplit = 0; out->part = nullptr; out->cnt = nullptr;   // no key split unless the caller sets one
   }
   return P0K_OK;
 }

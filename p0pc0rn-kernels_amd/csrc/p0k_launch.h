@@ -33,16 +33,8 @@ struct AttnParams {
   uint16_t *O;                 // [Lq][ldo] f16, head h at column h * 128
   uint32_t Lq, Lk, ldo, Hq, Hkv, mode, nvalid;
   float scale, cap;            // natural-log scale; cap > 0: scores -> cap * tanh(scores / cap)
-  // key split of the last round: query blocks [0, t0) run whole, the nsplit blocks after them as two halves of
-  // their key range each, meeting in `part` with one arrival counter per block in `cnt` (zero before and after)
-  uint32_t t0, nsplit;
-  float *part;
-  uint32_t *cnt;
 };
 int attention_bq(uint32_t Lq, uint32_t Hq, int cus);   // queries per workgroup
-// the key split for a call (t0, nsplit as above) and the workspace it needs
-void attention_split(const AttnParams &p, int cus, uint32_t *t0, uint32_t *nsplit);
-uint64_t attention_part_bytes(const AttnParams &p, int cus, uint32_t nsplit);
 hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s);
 // pixstats and GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109)
 hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, float *r, hipStream_t s);

@@ -459,14 +459,6 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
       (r = check_live(c, a->v_buf, a->v_size, "attention", "v")) || (r = check_live(c, a->o_buf, a->o_size, "attention", "o")))
     return r;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  p0k::attention_split(p, p0k::MI355X_CUS, &p.t0, &p.nsplit);
-  if (p.nsplit) {
-    if (p.nsplit > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "attention: too many split query blocks");
-    const uint64_t need = p0k::attention_part_bytes(p, p0k::MI355X_CUS, p.nsplit);
-    if (int rr = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "attention split")) return rr;
-    p.part = c->ws_part;
-    p.cnt = c->ws_cnt;
-  }
   hipError_t e = p0k::launch_attention(p, p0k::MI355X_CUS, c->stream);
   if (e != hipSuccess) return hip_err(e, "attention launch");
   return P0K_OK;
