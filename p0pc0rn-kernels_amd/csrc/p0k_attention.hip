@@ -6,8 +6,9 @@
 //   i iff j <= min(i, nvalid - 1); 2: j < nvalid. Scores s = scale * q.k (scale defaults to 1/sqrt(128)), optionally
 //   soft-capped to cap * tanh(s / cap); O = softmax(s) V with an exact online softmax in fp32.
 //
-// One workgroup owns 128 or 256 queries of one head (4 or 8 waves, 32 queries each; each wave keeps its Q rows in
-// registers). Everything is computed transposed, so that a lane owns ONE query and the softmax statistics stay in it:
+// One workgroup owns 128 queries of one head (4 waves, 32 queries each, two workgroups per CU; a 256-query, 8-wave
+// variant is selectable for tuning); each wave keeps its Q rows in registers. Everything is computed transposed, so
+// that a lane owns ONE query and the softmax statistics stay in it:
 //   S^T (keys x queries) = K Q^T           v_mfma_f32_32x32x16_f16, A = K from LDS, B = Q^T from registers
 //   O^T (d x queries)   += V^T P           A = V^T from LDS, B = P = exp(S - m) from the S^T registers (fp16)
 // In the 32x32 layout lane l holds column l % 32 (its query) and 16 rows 8 (r/4) + 4 (l/32) + r%4, so a row maximum
@@ -17,7 +18,7 @@
 // by the load-to-LDS path in their HBM layout [key][d], and the V^T operand is read with the transposing
 // ds_read_b64_tr_b16 (four keys of one d per lane). Both tiles are XOR-swizzled so the 16-byte K reads and the
 // transposed V reads of a wave hit distinct banks. Two waves per SIMD (256 registers each) let one wave's softmax
-// run under the other's MFMAs; with 256 queries a K / V tile is fetched into LDS once per 256 queries instead of 128.
+// run under the other's MFMAs.
 #include "p0k_device.h"
 #include "p0k_launch.h"
 #include <cstdlib>
@@ -248,8 +249,13 @@ int attention_bq(uint32_t Lq, uint32_t Hq, int cus) {
     const int v = atoi(ov);
     if (v == 128 || v == 256) return v;
   }
-  // 256 queries share each K / V tile (half the LDS fill per query) once that still gives every CU a workgroup
-  return (uint64_t)((Lq + 255) / 256) * Hq >= (uint64_t)cus ? 256 : 128;
+  // 128 (two workgroups per CU). 256 queries per workgroup halve the LDS fill per query but run one workgroup per CU:
+  // 24 heads x 4096 queries, 300 us vs 280 us (its 384 blocks leave half the CUs idle in the second round, where
+  // the 768 blocks of 128 let the last third of a CU's blocks run alone and faster)
+  (void)Lq;
+  (void)Hq;
+  (void)cus;
+  return 128;
 }
 
 hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s) {
