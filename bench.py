@@ -5,11 +5,13 @@
 A step is one gemm call (one pass of the hot path over one batch of synthetic input, all inputs resident in HBM).
 The headline line is the q4 GEMV decode with the SwiGLU epilogue at M = 1 (weight rows 28672 =
 gate 14336 | up 14336, K 4096): `value` is its HBM throughput in GB/s of algorithmic bytes. The same JSON line carries
-every other config (decode M = 4 and 16, q8 prefill with RMSNorm + residual, the DiT QKV / GeGLU GEMMs, conv3) under
-"workloads", each with its own roofline fraction.
+every other config under "workloads", each with its own roofline fraction: decode M = 4 and 16, the plain q4 GEMV
+N 14336, q8 prefill with RMSNorm + fp32 residual add (and its fp16-residual `bias` + `res` variant, and the rowstats
+pass it needs, timed on its own), the DiT QKV / GeGLU GEMMs, conv3 and the attention consumer.
 
 Timing: the timed calls are captured once in a HIP graph on the library's stream and replayed; HIP events on that
-stream bracket the replays (p0k_sync before and after). For the HBM-bound decode the calls rotate through enough
+stream bracket the replays (p0k_sync before and after), one before each replay, so every workload also reports the
+p10 / median / p90 of its per-call time over the replays. For the HBM-bound decode the calls rotate through enough
 weight copies (> 256 MB) that no call finds its weights in the MALL. Inputs come from numpy's PCG64 generator with
 fixed seeds, encoded with libp0k's own FORMAT.md encoders (BASELINE.json value recipes).
 
@@ -69,10 +71,11 @@ class Workload:
         self.M, self.args, self.bufs, self.extra, self.kind = M, args, bufs, extra or {}, kind
 
 
-def decode_q4(dev, M, copies=None):
-    """q4 GEMV decode, out 14336 with SwiGLU (weight rows [gate 14336 | up 14336]), K 4096."""
+def decode_q4(dev, M, copies=None, glu=True):
+    """q4 GEMV decode, out 14336 with SwiGLU (weight rows [gate 14336 | up 14336]), K 4096; glu=False:
+    the plain q4 GEMV N 14336 (36.7 MB of weights) with the f16 epilogue."""
     N_out, K = 14336, 4096
-    rows = 2 * N_out
+    rows = 2 * N_out if glu else N_out
     r = rng(1)
     W = (r.standard_normal((rows, K), dtype=np.float32) * np.float32(0.02))
     wb = p0k.pack("q4g32a.t64", W, rows, K)
@@ -85,7 +88,14 @@ def decode_q4(dev, M, copies=None):
     args = [{"w": {"enc": "q4g32a.t64", "buf": b, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
              "x": {"buf": x}, "y": {"buf": y, "ld": N_out}, "M": M, "N": rows, "K": K, "epi": "swiglu", "wr0": 0,
              "wr1": N_out} for b in bufs[:copies]]
+    if not glu:
+        for a in args:
+            a.update(epi="f16")
+            del a["wr1"]
     nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
+    if not glu:
+        return Workload(f"decode_q4_plain_M{M}", f"q4 GEMV, M={M}, N={N_out}, K={K}, f16 epilogue", "hbm",
+                        2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
     return Workload(f"decode_q4_swiglu_M{M}", f"q4 GEMV + SwiGLU, M={M}, out {N_out}, weight rows {rows}, K={K}",
                     "hbm", 2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
 
@@ -110,6 +120,43 @@ def prefill_q8(dev):
     nbytes = wb.nbytes + M * K * 4 + 2 * M * N * 4 + M * 8 + K * 4
     return Workload("prefill_q8_rms_resadd", "q8 GEMM M=2048 N=4096 K=4096, RMSNorm prologue, fp32 residual add",
                     "mfma", 2.0 * M * N * K, nbytes, M, args, [xw, st, gam, R, w])
+
+
+def prefill_q8_f16res(dev):
+    """configs[2], the fp16-residual variant: the same q8 GEMM and RMSNorm prologue with the `bias` epilogue in place
+    over an fp16 residual (`res`, zero bias): Y_f16 = f16(acc + 0 + Y_f16)."""
+    M, N, K = 2048, 4096, 4096
+    r = rng(2)
+    W = r.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    wb = p0k.pack("q8g64s.t64", W, N, K)
+    del W
+    xw = dev.upload(f16(r.standard_normal(M * K)).astype(np.float32))
+    st = dev.buffer(M * 8)
+    dev.rowstats(xw, M, K, "rms", 1e-6, st)
+    gam = dev.upload((1 + 0.1 * r.standard_normal(K)).astype(np.float32))
+    R = dev.upload(f16(r.standard_normal(M * N)))
+    bias = dev.buffer(N * 4)
+    w = dev.upload(wb)
+    args = [{"w": {"enc": "q8g64s.t64", "buf": w, "off": 0, "bytes": wb.nbytes, "rows": N, "cols": K},
+             "x": {"buf": xw, "mode": "rms"}, "stats": {"buf": st}, "pv": {"buf": gam},
+             "ev": {"buf": bias}, "y": {"buf": R}, "M": M, "N": N, "K": K, "epi": "bias", "res": True}]
+    nbytes = wb.nbytes + M * K * 4 + 2 * M * N * 2 + M * 8 + K * 4 + N * 4
+    return Workload("prefill_q8_rms_bias_f16res", "q8 GEMM M=2048 N=4096 K=4096, RMSNorm prologue, fp16 residual "
+                    "(bias epilogue in place, zero bias)", "mfma", 2.0 * M * N * K, nbytes, M, args,
+                    [xw, st, gam, R, bias, w])
+
+
+def prefill_rowstats(dev):
+    """configs[2]'s rowstats pass on its own: RMS statistics of the fp32 x (2048 x 4096, 33.5 MB read)."""
+    M, K = 2048, 4096
+    r = rng(2)
+    x = f16(r.standard_normal(M * K)).astype(np.float32)
+    copies = -(-(2 * MALL) // x.nbytes)                 # rotate copies past the MALL, as for the decode weights
+    xs = [dev.upload(x) for _ in range(copies)]
+    st = dev.buffer(M * 8)
+    args = [{"x": xw, "rows": M, "cols": K, "mode": "rms", "eps": 1e-6, "st": st} for xw in xs]
+    return Workload("prefill_rowstats_rms", "rowstats (RMS) of configs[2]'s fp32 x, 2048 x 4096", "hbm", 3.0 * M * K,
+                    M * K * 4 + M * 8, M, args, xs + [st], {"x_copies": copies}, kind="rowstats")
 
 
 def rope2d(L, grid_w, theta=10000.0):
@@ -197,7 +244,9 @@ def dit_attn(dev):
 
 BUILDERS = {
     "decode1": lambda d: decode_q4(d, 1), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
-    "prefill": prefill_q8, "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
+    "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
+    "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
+    "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
 }
 
 
@@ -210,6 +259,9 @@ def time_workload(dev, wl, steps, warmup):
         run = dev.attention_raw
         for s in structs:
             p0k._chk(L.p0k_attention_check(C.byref(s)))
+    elif wl.kind == "rowstats":
+        structs = wl.args
+        run = lambda a: dev.rowstats(a["x"], a["rows"], a["cols"], a["mode"], a["eps"], a["st"])   # noqa: E731
     else:
         structs = [p0k.gemm_args(a, dev.resolve) for a in wl.args]
         run = dev.gemm_raw
@@ -228,7 +280,7 @@ def time_workload(dev, wl, steps, warmup):
         ms = dev.elapsed_ms(e0, e1) / steps
         dev.event_destroy(e0)
         dev.event_destroy(e1)
-        return ms, ms, steps
+        return ms, ms, steps, None
     per_graph = max(len(structs), min(steps, 64 if wl.bound == "hbm" else 8))
     per_graph -= per_graph % len(structs)
     dev.graph_begin()
@@ -241,20 +293,25 @@ def time_workload(dev, wl, steps, warmup):
     for _ in range(max(1, -(-warmup // per_graph))):
         dev.graph_launch(g)
     dev.done()
-    e0, e1 = dev.event(), dev.event()
+    # one event before each replay and one after the last: the whole timed region, and per replay the time per call
+    ev = [dev.event() for _ in range(reps + 1)]
     t0 = time.perf_counter()
-    dev.record(e0)
-    for _ in range(reps):
+    dev.record(ev[0])
+    for i in range(reps):
         dev.graph_launch(g)
-    dev.record(e1)
+        dev.record(ev[i + 1])
     dev.done()
     wall = time.perf_counter() - t0
-    ms = dev.elapsed_ms(e0, e1)
-    dev.event_destroy(e0)
-    dev.event_destroy(e1)
+    ms = dev.elapsed_ms(ev[0], ev[-1])
+    per = sorted(dev.elapsed_ms(ev[i], ev[i + 1]) / per_graph for i in range(reps))
+    for e in ev:
+        dev.event_destroy(e)
     dev.graph_destroy(g)
     n = reps * per_graph
-    return ms / n, wall / n * 1e3, n
+    q = lambda f: per[min(reps - 1, int(f * reps))]   # noqa: E731
+    dist = {"p10": round(q(0.1), 5), "median": round(q(0.5), 5), "p90": round(q(0.9), 5), "replays": reps,
+            "calls_per_replay": per_graph}
+    return ms / n, wall / n * 1e3, n, dist
 
 
 def roofline(wl, ms):
@@ -332,9 +389,10 @@ def main():
     for n in names:
         wl = BUILDERS[n](dev)
         steps = a.steps if wl.bound == "hbm" else max(10, a.steps // 10)
-        ms, wall_ms, count = time_workload(dev, wl, steps, a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10))
+        ms, wall_ms, count, dist = time_workload(dev, wl, steps, a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10))
         rf = roofline(wl, ms)
         res = {"name": wl.name, "desc": wl.desc, "M": wl.M, "ms_per_call": round(ms, 5), "calls": count,
+               "ms_per_call_dist": dist,
                "tflops": round(wl.flops / ms / 1e9, 3), "gbps": round(wl.algo_bytes / ms / 1e6, 1),
                "algo_bytes": wl.algo_bytes, "flops": wl.flops, "roofline": rf, **wl.extra}
         log(f"{wl.name}: {ms * 1e3:.2f} us/call  {res['gbps']} GB/s  {res['tflops']} TFLOP/s  frac {rf['frac']}")

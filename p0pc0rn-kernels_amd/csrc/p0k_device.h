@@ -351,10 +351,21 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
       const float *b = p.EV + p.evOff + col;
       const uint16_t *yh = (const uint16_t *)p.Y + yi;
       const bool res = p.flags & F_RES;
-      for (uint32_t j = 0; j < 8 && j < nv; j++) {
-        float t = v[j] + b[j];
-        if (res) t += h_val(yh[j]);
-        v[j] = t;
+      if (nv >= 8 && (((uintptr_t)yh) & 15u) == 0) {                 // whole 16-byte groups: one residual load
+        const u32x4 r = res ? *(const u32x4 *)yh : (u32x4){0u, 0u, 0u, 0u};
+        const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          float t = v[j] + b[j];
+          if (res) t += h_val((uint16_t)(rw[j >> 1] >> (16 * (j & 1))));
+          v[j] = t;
+        }
+      } else {
+        for (uint32_t j = 0; j < 8 && j < nv; j++) {
+          float t = v[j] + b[j];
+          if (res) t += h_val(yh[j]);
+          v[j] = t;
+        }
       }
       store_f16x8(p.Y, yi, v, nv);
     } else {                                                                       // R += gate[n] * (acc + bias[n])
