@@ -4,8 +4,9 @@
 // matrix core uses them.
 //
 // One workgroup computes a TBM x TBN tile (TBM, TBN in {128, 256}): 4 waves (2 x 2) for the smaller tiles, 8 waves
-// (2 x 4, two per SIMD, so one wave's decode and LDS reads run under the other's MFMAs) for 256 x 256; a wave owns
-// (TBM/2) x (TBN/2) or 128 x 64 as 32x32 v_mfma_f32_32x32x16_f16 blocks. K moves in steps of 64 through a ring of S LDS stages:
+// (2 x 4, two per SIMD, so one wave's decode and LDS reads run under the other's MFMAs) for 256 x 256 and, with f16
+// or q8 weights, 256 x 128; a wave owns (TBM/2) x (TBN/2), 128 x 64 or 128 x 32 as 32x32 v_mfma_f32_32x32x16_f16
+// blocks. K moves in steps of 64 through a ring of S LDS stages:
 //   X' rows      [row][128 B], the 16-byte chunk c of row r at c ^ ((r >> 1) & 7)
 //   f16 weights  the same layout, one row per ws column
 //   q4 records   per 64-column block and 32-k record: the 64 code rows [col][16 B] as stored, and the 64 (scale, min)
@@ -462,7 +463,11 @@ hipError_t launch_dma_one(const Params &p, hipStream_t s) {
 template <int WE, int XG>
 hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
   if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256, 8>(p, s);
-  if (bm == 256 && bn == 128) return launch_dma_one<WE, XG, 256, 128>(p, s);
+  if (bm == 256 && bn == 128) {
+    // 8 waves (2 x 4, each 128 x 32) where the stage's DMA splits over 8 waves (q4's 4 code instructions do not)
+    if constexpr (WE != W_Q4) return launch_dma_one<WE, XG, 256, 128, 8>(p, s);
+    else return launch_dma_one<WE, XG, 256, 128>(p, s);
+  }
   if (bm == 128 && bn == 256) return launch_dma_one<WE, XG, 128, 256>(p, s);
   if (bm == 128 && bn == 128) return launch_dma_one<WE, XG, 128, 128>(p, s);
   return hipErrorInvalidValue;
@@ -537,20 +542,21 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn) {
   auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
     if (m == 256 && n == 256) return 1;
+    if (m == 256 && we != W_Q4) return 1;                            // 8 waves
     if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
     if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
     return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
   };
-  // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: 256 x 256 runs 8 waves
-  // (two per SIMD), the others 4; the quantised weights favour 256-row tiles (each decoded weight feeds four 32-row
-  // blocks instead of two)
+  // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: 256 x 256 and (f16, q8)
+  // 256 x 128 run 8 waves (two per SIMD), the others 4; the quantised weights favour 256-row tiles (each decoded
+  // weight feeds four 32-row blocks instead of two)
   struct C { unsigned m, n; double rate; };
-  const C c16[] = {{256, 256, 1.0}, {128, 256, 0.94}, {256, 128, 0.92}, {128, 128, 0.91}};
+  const C c16[] = {{256, 256, 1.0}, {128, 256, 0.94}, {256, 128, 0.99}, {128, 128, 0.91}};
   const C cq4[] = {{256, 256, 1.0}, {128, 256, 0.68}, {256, 128, 0.91}, {128, 128, 0.68}};
-  const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.75}, {256, 128, 0.78}, {128, 128, 0.78}};
-  // the conv3 gather computes each row's tap address per step: two workgroups of 128 x 128 per CU hide it best
-  // (f16 weights, 13 x 92 x 160 x 128 clip: 128 x 128 252 us, 256 x 128 272, 256 x 256 382, 128 x 256 409)
-  const C cg[] = {{256, 256, 0.66}, {128, 256, 0.62}, {256, 128, 0.93}, {128, 128, 1.0}};
+  const C cq8[] = {{256, 256, 1.0}, {128, 256, 0.75}, {256, 128, 0.84}, {128, 128, 0.78}};
+  // the conv3 gather computes each row's tap address per step (f16 weights, 13 x 92 x 160 x 128 clip: 256 x 128 with
+  // 8 waves 244 us, 128 x 128 (two workgroups per CU) 257, 256 x 256 382 and 128 x 256 409 with 4 waves)
+  const C cg[] = {{256, 256, 0.66}, {128, 256, 0.62}, {256, 128, 1.05}, {128, 128, 1.0}};
   const C *cand = xg == X_CONV3 ? cg : (we == W_F16 ? c16 : (we == W_Q4 ? cq4 : cq8));
   double best = -1.0;
   for (int ci = 0; ci < 4; ci++) {

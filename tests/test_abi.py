@@ -175,8 +175,8 @@ def test_dma_tile_choice(enc, M, N, tile):
 
 
 def test_conv3_gather_tile_choice():
-    """conv3 with Ci % 64 == 0 takes the load-to-LDS gather, 128 x 128 tiles (two workgroups per CU hide the per-step
-    tap addressing); Ci = 32 keeps the register-staged kernel."""
-    t = p0k.select_tile(host_args(make_conv3_case(T=4, H=46, W=80, C=64, N=128)))
-    assert t["kernel"] == "mfma_dma" and (t["BM"], t["BN"]) == (128, 128)
+    """conv3 with Ci % 64 == 0 takes the load-to-LDS gather, 256 x 128 tiles (8 waves: the per-step tap addressing
+    runs under the other wave's MFMAs); Ci = 32 keeps the register-staged kernel."""
+    t = p0k.select_tile(host_args(make_conv3_case(T=13, H=92, W=160, C=128, N=128)))
+    assert t["kernel"] == "mfma_dma" and (t["BM"], t["BN"]) == (256, 128)
     assert p0k.select_tile(host_args(make_conv3_case(T=4, H=6, W=8, C=32, N=128)))["kernel"] == "mfma"
