@@ -53,6 +53,7 @@ struct Params {
   uint32_t tilesM, tilesN;
   const uint8_t *Z;    // 16 zero bytes (the load-to-LDS conv3 gather reads them for padding taps)
   uint32_t nvox;       // conv3: input voxels the call may read (frames x Hi x Wi)
+  uint32_t nbase;      // load-to-LDS GEMM: first ws column of this launch (its tiles cover [nbase, N))
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }

@@ -164,7 +164,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV>::OCC), (DT<WE, TBM, TB
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint32_t mt, nt;
   tile_order(p, blockIdx.x, mt, nt);
-  const uint32_t mB = mt * TBM, nB = nt * TBN;
+  const uint32_t mB = mt * TBM, nB = p.nbase + nt * TBN;
   const uint32_t nk = p.K / DBK;
 
   // ---- per-lane DMA sources (step 0) and per-step advances; instruction t of this wave is number 4 t + wave of
@@ -455,7 +455,7 @@ template <int WE, int XG, int TBM, int TBN, int NWV = 4>
 hipError_t launch_dma_one(const Params &p, hipStream_t s) {
   Params q = p;
   q.tilesM = (p.M + TBM - 1) / TBM;
-  q.tilesN = (p.N + TBN - 1) / TBN;
+  q.tilesN = (p.N - p.nbase + TBN - 1) / TBN;
   hipLaunchKernelGGL((k_gemm_dma<WE, XG, TBM, TBN, NWV>), dim3(q.tilesM * q.tilesN), dim3(64 * NWV), 0, s, q);
   return hipGetLastError();
 }
@@ -539,14 +539,16 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 
 // The tile: each candidate scored by its relative per-CU rate times the fraction of workgroup slots (one or two per
 // CU, as the tile's LDS allows) that hold real work over the rounds the grid needs.
+static unsigned dma_wgs(int we, unsigned m, unsigned n) {           // workgroups per CU
+  if (m == 256 && n == 256) return 1;
+  if (m == 256 && we != W_Q4) return 1;                              // 8 waves
+  if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
+  if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
+  return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
+}
+
 void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn) {
-  auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
-    if (m == 256 && n == 256) return 1;
-    if (m == 256 && we != W_Q4) return 1;                            // 8 waves
-    if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
-    if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
-    return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
-  };
+  auto per_cu = [&](unsigned m, unsigned n) -> unsigned { return dma_wgs(we, m, n); };
   // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: 256 x 256 and (f16, q8)
   // 256 x 128 run 8 waves (two per SIMD), the others 4; the quantised weights favour 256-row tiles (each decoded
   // weight feeds four 32-row blocks instead of two)
@@ -571,7 +573,50 @@ void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm
   }
 }
 
+static hipError_t launch_dma_x(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s) {
+  switch (we) {
+  case W_Q4: return launch_dma_we<W_Q4, X_F16>(p, bm, bn, s);
+  case W_Q8: return launch_dma_we<W_Q8, X_F16>(p, bm, bn, s);
+  case W_F16: return launch_dma_we<W_F16, X_F16>(p, bm, bn, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Tail columns: when the grid's last round of tiles would leave at least half of the workgroup slots empty, the
+// whole rounds run as one launch over the first columns (as many whole column bands of tiles as they hold) and the
+// remaining columns as a second launch with the tile dma_tile picks for them (smaller tiles, more of them). Every tile
+// sums K in the same order, so the output is the same bits as one launch. DiT QKV (576 tiles of 256 x 256 on 256 CUs,
+// 2.25 rounds): 512 tiles, then the last 1024 columns in 128 x 128 tiles. P0K_DMA_TAIL=0 keeps one launch.
+void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned cus, uint32_t *ncut, unsigned *bm2,
+              unsigned *bn2) {
+  *ncut = N;
+  *bm2 = bm;
+  *bn2 = bn;
+  if (const char *ov = getenv("P0K_DMA_TAIL"))
+    if (atoi(ov) == 0) return;
+  const uint32_t tilesM = (M + bm - 1) / bm, tilesN = (N + bn - 1) / bn, T = tilesM * tilesN;
+  const uint32_t slots = cus * dma_wgs(we, bm, bn), full = T / slots * slots, tail = T - full;
+  if (tail == 0 || 2 * tail > slots || full < tilesM) return;
+  const uint32_t nA = full / tilesM;                           // column bands of the first launch
+  if (nA >= tilesN) return;
+  *ncut = nA * bn;
+  dma_tile(M, N - *ncut, we, X_F16, cus, bm2, bn2);
+}
+
 hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s) {
+  if (xg != X_CONV3) {
+    uint32_t ncut;
+    unsigned bm2, bn2;
+    dma_tail(p.M, p.N, we, bm, bn, MI355X_CUS, &ncut, &bm2, &bn2);
+    if (ncut >= p.N) return launch_dma_x(p, we, bm, bn, s);
+    Params a = p, b = p;
+    a.N = ncut;                                                 // epilogue bounds: the first launch's columns only
+    a.nbase = 0;
+    b.nbase = ncut;
+    hipError_t e = launch_dma_x(a, we, bm, bn, s);
+    if (e != hipSuccess) return e;
+    return launch_dma_x(b, we, bm2, bn2, s);
+  }
   if (xg == X_CONV3) {
     switch (we) {
     case W_Q4: return launch_dma_we<W_Q4, X_CONV3>(p, bm, bn, s);
@@ -579,11 +624,6 @@ hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigne
     case W_F16: return launch_dma_we<W_F16, X_CONV3>(p, bm, bn, s);
     }
     return hipErrorInvalidValue;
-  }
-  switch (we) {
-  case W_Q4: return launch_dma_we<W_Q4, X_F16>(p, bm, bn, s);
-  case W_Q8: return launch_dma_we<W_Q8, X_F16>(p, bm, bn, s);
-  case W_F16: return launch_dma_we<W_F16, X_F16>(p, bm, bn, s);
   }
   return hipErrorInvalidValue;
 }

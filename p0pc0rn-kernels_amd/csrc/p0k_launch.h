@@ -16,6 +16,10 @@ hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsign
 // launch_xprep over the input voxels; K % 64 == 0). dma_tile picks the tile. xg: X_F16 (rows) or X_CONV3.
 bool gemm_dma_ok(const Params &p, int we, int xm, uint64_t wbytes);
 void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn);
+// the column split launch_gemm_dma makes for a mostly empty last round: columns [0, ncut) with the chosen tile, the
+// rest with bm2 x bn2 (ncut == N: one launch)
+void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned cus, uint32_t *ncut, unsigned *bm2,
+              unsigned *bn2);
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s);
 hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace

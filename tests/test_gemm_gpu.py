@@ -313,6 +313,37 @@ def test_every_mfma_tile_matches_oracle(dev, kw, kernel, monkeypatch):
         assert np.array_equal(o, outs[0])
 
 
+@pytest.mark.parametrize("kw", [dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=4096, N=4352, K=128, Hq=32, Hkv=1),
+                                dict(enc="q8g64s.t64", epi="swiglu", M=4100, N=4608, K=64, bias=True)],
+                         ids=["q4-lnmod-heads", "q8-swiglu"])
+def test_tail_columns_bit_identical(dev, kw, monkeypatch):
+    """A grid whose last round of tiles would be mostly empty runs as two launches: whole column bands of the chosen
+    tile, then the remaining columns with smaller tiles. Every tile sums K in the same order, so the result is the
+    same bits as one launch (P0K_DMA_TAIL=0)."""
+    c = make_case(seed=24, **kw)
+    banner(f"tail columns {kw}")
+    monkeypatch.setenv("P0K_DMA_TAIL", "0")
+    one = c.run_device(dev)
+    monkeypatch.delenv("P0K_DMA_TAIL")
+    two = c.run_device(dev)
+    assert np.array_equal(one, two)
+    rows = [(0, 8), (kw["M"] - 8, kw["M"])]
+    want = c.bufs[c.out].copy()
+    for m0, m1 in rows:
+        o = c.run_oracle(m0, m1)
+        if kw["epi"] == "heads":
+            nh = kw["Hq"] + 2 * kw["Hkv"]
+            want.reshape(nh, -1, 128)[:, m0:m1] = o.reshape(nh, -1, 128)[:, m0:m1]
+        else:
+            want.reshape(kw["M"], -1)[m0:m1] = o.reshape(kw["M"], -1)[m0:m1]
+    for m0, m1 in rows:
+        if kw["epi"] == "heads":
+            nh = kw["Hq"] + 2 * kw["Hkv"]
+            assert_close(two.reshape(nh, -1, 128)[:, m0:m1], want.reshape(nh, -1, 128)[:, m0:m1], what="tail rows")
+        else:
+            assert_close(two.reshape(kw["M"], -1)[m0:m1], want.reshape(kw["M"], -1)[m0:m1], what="tail rows")
+
+
 @pytest.mark.parametrize("t", MFMA_TILES)
 def test_conv3_every_mfma_tile_bit_identical(dev, t, monkeypatch):
     c = make_conv3_case(T=3, H=10, W=12, C=32, N=256, pn=True)
