@@ -489,15 +489,14 @@ __global__ __launch_bounds__(256) void k_pnprep(Params p, uint16_t *xp) {
   }
 }
 
-// X' of the rms / lnmod prologues, materialised once: Xp[m][k] = xload8 (the fused prologue's exact values)
+// X' of the rms / lnmod prologues, materialised once: Xp[m][k] = xload8 (the fused prologue's exact values); one
+// workgroup per row, 8 k per thread and step
 template <int XM>
 __global__ __launch_bounds__(256) void k_xprep(Params p, uint16_t *xp) {
-  const uint32_t k8 = p.K / 8;
-  const uint64_t n = (uint64_t)p.M * k8;
-  for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < n; t += (uint64_t)gridDim.x * 256) {
-    const uint32_t m = (uint32_t)(t / k8), kq = (uint32_t)(t - (uint64_t)m * k8);
-    *(u32x4 *)(xp + (size_t)m * p.K + 8 * kq) = xload8<XM, 1>(p, m, RowCtx{0, 0, 0}, 8 * kq);
-  }
+  const uint32_t k8 = p.K / 8, m = blockIdx.x;
+  uint16_t *dst = xp + (size_t)m * p.K;
+#pragma unroll 2
+  for (uint32_t kq = threadIdx.x; kq < k8; kq += 256) *(u32x4 *)(dst + 8 * kq) = xload8<XM, 1>(p, m, RowCtx{0, 0, 0}, 8 * kq);
 }
 
 }  // namespace
@@ -529,10 +528,9 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
     if (n) hipLaunchKernelGGL(k_pnprep, dim3(blocks), dim3(256), 0, s, p, xp);
     return hipGetLastError();
   }
-  const uint64_t n = (uint64_t)p.M * (p.K / 8);
-  const unsigned blocks = (unsigned)(n / 256 < 4096 ? (n + 255) / 256 : 4096);
-  if (xm == X_RMS) hipLaunchKernelGGL(k_xprep<X_RMS>, dim3(blocks), dim3(256), 0, s, p, xp);
-  else if (xm == X_LNMOD) hipLaunchKernelGGL(k_xprep<X_LNMOD>, dim3(blocks), dim3(256), 0, s, p, xp);
+  if (p.M == 0) return hipSuccess;
+  if (xm == X_RMS) hipLaunchKernelGGL(k_xprep<X_RMS>, dim3(p.M), dim3(256), 0, s, p, xp);
+  else if (xm == X_LNMOD) hipLaunchKernelGGL(k_xprep<X_LNMOD>, dim3(p.M), dim3(256), 0, s, p, xp);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
