@@ -5,7 +5,7 @@
 A step is one gemm call (one pass of the hot path over one batch of synthetic input, all inputs resident in HBM).
 The headline line is the q4 GEMV decode with the SwiGLU epilogue at M = 1 (weight rows 28672 =
 gate 14336 | up 14336, K 4096): `value` is its HBM throughput in GB/s of algorithmic bytes. The same JSON line carries
-every other config under "workloads", each with its own roofline fraction: decode M = 4 and 16, the plain q4 GEMV
+every other config under "workloads", each with its own roofline fraction: decode M = 2, 4, 8 and 16, the plain q4 GEMV
 N 14336, q8 prefill with RMSNorm + fp32 residual add (and its fp16-residual `bias` + `res` variant, and the rowstats
 pass it needs, timed on its own), the DiT QKV / GeGLU GEMMs, conv3 and the attention consumer.
 
@@ -244,6 +244,7 @@ def dit_attn(dev):
 
 BUILDERS = {
     "decode1": lambda d: decode_q4(d, 1), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
+    "decode2": lambda d: decode_q4(d, 2), "decode8": lambda d: decode_q4(d, 8),
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
     "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,

@@ -230,10 +230,11 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
     // and addresses the tensor with 32-bit offsets
     if ((we != P0K_ENC_Q8G64S_T64 || a->wk0 % 64 == 0) && (we != P0K_ENC_F16 || (f & F_WALIGN8)) &&
         wbytes < (1ull << 32)) {
-      // one q4 row: the VALU stream (exact dot products of fp32-dequantised weights; one 16-byte load covers 16
-      // whole code rows); 2..16 rows, and q8 / f16 at any M <= 16: the matrix cores (their per-block loads read whole
-      // record rows, where a row per lane would read 16 of every 64 bytes per load: q8 2.8 vs 3.6 TB/s, f16 1.4 vs 3.7)
-      bool mf = M >= 2 || we != P0K_ENC_Q4G32A_T64;
+      // one or two q4 rows: the VALU stream (exact dot products of fp32-dequantised weights; one 16-byte load covers
+      // 16 whole code rows; at M = 2, 19-20 us vs 20-22 on the matrix cores for N 28672, K 4096); 3..16 rows, and q8 /
+      // f16 at any M <= 16: the matrix cores (the VALU stream's work grows with M: 31 vs 22 us at M = 4; and for q8 /
+      // f16 its per-lane loads read 16 of every 64 bytes per load: q8 2.8 vs 3.6 TB/s, f16 1.4 vs 3.7)
+      bool mf = M >= 3 || we != P0K_ENC_Q4G32A_T64;
       if (const char *ov = getenv("P0K_GEMV_MF")) mf = mf && atoi(ov) != 0;   // tuning: the VALU stream for M > 1
       gemv_split(p, we, MI355X_CUS, mf, &S, &KS);
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave

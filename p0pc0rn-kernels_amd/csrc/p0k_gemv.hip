@@ -292,7 +292,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Decode on the matrix cores (2 <= M <= 16). With several rows of X the per-row dot products of the stream above
+// Decode on the matrix cores (3 <= M <= 16 for q4, M <= 16 for q8 / f16). With several rows of X the per-row dot products of the stream above
 // multiply its VALU work; here the same items, waves and ring feed v_mfma_f32_16x16x32_f16 instead. Per 32-k step
 // (q4, f16; 64-k for q8) a wave runs one MFMA per block of 16 of its 64 weight rows: A = X' (16 rows, zero past M),
 // B = the block's weights. Lane l supplies, for block i, weight row 16 i + l%16 and the 8 k at 8 (l/16) of the step

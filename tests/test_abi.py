@@ -131,6 +131,8 @@ def test_kernel_choice():
     assert p0k.select_tile(host_args(make_case(M=1, enc="q4g32a.t64")))["kernel"] == "gemv"
     assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv_mfma"              # f16 / q8 rows: matrix cores
     assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
+    assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, two rows: VALU
+    assert p0k.select_tile(host_args(make_case(M=3, enc="q4g32a.t64")))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma_dma"          # fp16 rows, K % 64 == 0
     assert p0k.select_tile(host_args(make_case(M=17, K=96)))["kernel"] == "mfma"         # K % 64 != 0

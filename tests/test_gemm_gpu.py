@@ -87,7 +87,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    assert kern == ("gemv" if M == 1 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
+    assert kern == ("gemv" if M <= 2 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
