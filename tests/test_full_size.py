@@ -63,11 +63,24 @@ def test_decode_q4_swiglu_full(dev, M):
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"decode M={M}")
 
 
+@pytest.mark.parametrize("enc,epi,N", [("q8g64s.t64", "swiglu", 28672), ("f16", "swiglu", 28672),
+                                       ("q4g32a.t64", "f16", 14336)], ids=["q8-swiglu", "f16-swiglu", "q4-plain"])
+def test_decode_m1_other_weights_full(dev, enc, epi, N):
+    """configs[1]'s shape at M = 1 with q8 and f16 weights (the matrix-core GEMV), and the plain q4 GEMV N = 14336,
+    whose 112 column tiles split K in two and meet through the workspace; every output row."""
+    banner(f"full-size decode M=1 {enc} {epi} N={N}")
+    c = make_case(enc=enc, epi=epi, M=1, N=N, K=4096, seed=105, wscale=0.02)
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"decode M=1 {enc} {epi}")
+
+
 FULL = {
     "prefill_q8_rms_resadd": dict(enc="q8g64s.t64", xmode="rms", epi="resadd", M=2048, N=4096, K=4096, wscale=0.02),
     "dit_qkv_q4_lnmod_heads": dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=4096, N=9216, K=3072, Hq=24,
                                    Hkv=24, wscale=0.02),
     "dit_up_q4_geglu": dict(enc="q4g32a.t64", epi="swiglu", act="gelu", M=4096, N=24576, K=3072, wscale=0.02),
+    "prefill_q8_rms_bias_f16res": dict(enc="q8g64s.t64", xmode="rms", epi="bias", res=True, M=2048, N=4096, K=4096,
+                                       wscale=0.02),
 }
 
 
