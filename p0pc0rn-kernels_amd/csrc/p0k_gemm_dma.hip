@@ -44,7 +44,10 @@ struct DT {
   static constexpr int NIA = TBM / 8;
   static constexpr int NIC = WE == W_F16 ? TBN / 8 : (WE == W_Q4 ? NBLK * 2 : NBLK * 4);
   static constexpr int NIS = WE == W_F16 ? 0 : (WE == W_Q4 ? NBLK * 2 : NWV);
-  static_assert(NIA % NWV == 0 && NIC % NWV == 0 && NIS % NWV == 0, "DMA instructions per wave");
+  // the A instructions split evenly over the waves; the weight code and scale instructions together (a wave's one
+  // instruction may then be a code block for some waves and a scale block for others: q4 256 x 128 with 8 waves)
+  static_assert(NIA % NWV == 0 && (NIC + NIS) % NWV == 0, "DMA instructions per wave");
+  static constexpr bool WSPLIT = NIC % NWV == 0;                               // codes / scales on whole rounds
   static constexpr int NW = (NIA + NIC + NIS) / NWV;                           // per wave
   static constexpr int WA = NIA / NWV, WC = NIC / NWV;
   static constexpr int A_BYTES = TBM * 128;
@@ -197,8 +200,8 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV>::OCC), (DT<WE, TBM, TB
         src[t] = (m * p.ldx + p.kx0 + 8 * c) * 2u;
       }
       dst[t] = q * 1024;
-    } else if (t < T::WA + T::WC) {
-      const int b = q - NWV * T::WA;
+    } else if (T::WSPLIT ? t < T::WA + T::WC : q < T::NIA + T::NIC) {
+      const int b = q - T::NIA;
       if constexpr (WE == W_F16) {                    // weight rows of ws columns 8b .. 8b+7
         const uint32_t r = 8 * b + lane / 8, c = (lane & 7) ^ ((r >> 1) & 7);
         src[t] = (wrow(p, nB + r) * p.wG + p.wk0 + 8 * c) * 2u;
@@ -211,7 +214,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV>::OCC), (DT<WE, TBM, TB
       }
       dst[t] = T::A_BYTES + b * 1024;
     } else {
-      const int b = q - NWV * (T::WA + T::WC);
+      const int b = q - (T::NIA + T::NIC);
       if constexpr (WE == W_Q4) {                     // (scale, min) word of block b / 2, record b & 1
         const uint32_t r = wrow(p, nB + 64 * (b >> 1) + lane);
         src[t] = ((r >> 6) * p.wG + (p.wk0 >> 5) + (b & 1)) * 1280u + 1024u + (r & 63u) * 4u;
@@ -248,7 +251,7 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV>::OCC), (DT<WE, TBM, TB
         const size_t vox = ((size_t)it * p.Hi + (uint32_t)iy) * p.Wi + (uint32_t)ix;
         dma16a(in ? p.X + (vox * p.Ci + c0) * 2 + src[t] * 2 : p.Z, m0);
       } else if (t < T::WA) dma16(p.X + (size_t)kt * 128u, src[t], m0);
-      else if (t < T::WA + T::WC) dma16(p.W + (size_t)kt * WSTEP, src[t], m0);
+      else if (T::WSPLIT ? t < T::WA + T::WC : NWV * t + wave < T::NIA + T::NIC) dma16(p.W + (size_t)kt * WSTEP, src[t], m0);
       else dma4(p.W + (size_t)kt * WSTEP, src[t], m0);
     }
   };
@@ -464,9 +467,13 @@ template <int WE, int XG>
 hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
   if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256, 8>(p, s);
   if (bm == 256 && bn == 128) {
-    // 8 waves (2 x 4, each 128 x 32) where the stage's DMA splits over 8 waves (q4's 4 code instructions do not)
-    if constexpr (WE != W_Q4) return launch_dma_one<WE, XG, 256, 128, 8>(p, s);
-    else return launch_dma_one<WE, XG, 256, 128>(p, s);
+    // 8 waves (2 x 4, 128 x 32 each), one workgroup per CU; q4, whose 4-wave form fits two workgroups per CU, keeps
+    // that when the grid holds more than one tile per CU
+    if constexpr (WE == W_Q4) {
+      const uint64_t tiles = (uint64_t)((p.M + 255) / 256) * ((p.N - p.nbase + 127) / 128);
+      if (tiles > MI355X_CUS) return launch_dma_one<WE, XG, 256, 128, 4>(p, s);
+    }
+    return launch_dma_one<WE, XG, 256, 128, 8>(p, s);
   }
   if (bm == 128 && bn == 256) return launch_dma_one<WE, XG, 128, 256>(p, s);
   if (bm == 128 && bn == 128) return launch_dma_one<WE, XG, 128, 128>(p, s);
@@ -537,16 +544,19 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 
 // The tile: each candidate scored by its relative per-CU rate times the fraction of workgroup slots (one or two per
 // CU, as the tile's LDS allows) that hold real work over the rounds the grid needs.
-static unsigned dma_wgs(int we, unsigned m, unsigned n) {           // workgroups per CU
+// workgroups per CU of a tile for a grid of `tiles` (q4 256 x 128: 8 waves when the grid has one tile per CU at most)
+static unsigned dma_wgs(int we, unsigned m, unsigned n, uint64_t tiles, unsigned cus) {
   if (m == 256 && n == 256) return 1;
-  if (m == 256 && we != W_Q4) return 1;                              // 8 waves
+  if (m == 256 && (we != W_Q4 || tiles <= cus)) return 1;           // 8 waves
   if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
   if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
   return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
 }
 
 void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm, unsigned *bn) {
-  auto per_cu = [&](unsigned m, unsigned n) -> unsigned { return dma_wgs(we, m, n); };
+  auto per_cu = [&](unsigned m, unsigned n) -> unsigned {
+    return dma_wgs(we, m, n, (uint64_t)((M + m - 1) / m) * ((N + n - 1) / n), cus);
+  };
   // relative per-CU rates measured on MI355X at 4096^3 (f16 prologue), per weight encoding: 256 x 256 and (f16, q8)
   // 256 x 128 run 8 waves (two per SIMD), the others 4; the quantised weights favour 256-row tiles (each decoded
   // weight feeds four 32-row blocks instead of two)
@@ -566,7 +576,10 @@ void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm
     const uint64_t tiles = (uint64_t)((M + c.m - 1) / c.m) * ((N + c.n - 1) / c.n), slots = (uint64_t)cus * per_cu(c.m, c.n);
     const double rounds = (double)((tiles + slots - 1) / slots);
     const double useful = (double)M * N / ((double)c.m * c.n * rounds * slots);
-    const double score = c.rate * useful;
+    // q4 256 x 128 with 8 waves (a grid of one tile per CU at most): 2048 x 4096 x 4096 in 87.7 us against 143.7 for
+    // twice the work at 256 x 256
+    const double rate = (we == W_Q4 && c.m == 256 && c.n == 128 && tiles <= cus) ? 0.80 : c.rate;
+    const double score = rate * useful;
     if (score > best + 1e-9) { best = score; *bm = c.m; *bn = c.n; }
   }
 }
@@ -593,7 +606,7 @@ void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned
   if (const char *ov = getenv("P0K_DMA_TAIL"))
     if (atoi(ov) == 0) return;
   const uint32_t tilesM = (M + bm - 1) / bm, tilesN = (N + bn - 1) / bn, T = tilesM * tilesN;
-  const uint32_t slots = cus * dma_wgs(we, bm, bn), full = T / slots * slots, tail = T - full;
+  const uint32_t slots = cus * dma_wgs(we, bm, bn, T, cus), full = T / slots * slots, tail = T - full;
   if (tail == 0 || 2 * tail > slots || full < tilesM) return;
   const uint32_t nA = full / tilesM;                           // column bands of the first launch
   if (nA >= tilesN) return;
