@@ -172,8 +172,16 @@ const char *p0k_last_error(void);            /* message of the last failed call 
 int p0k_ctx_create(int device, p0k_ctx **out);
 void p0k_ctx_destroy(p0k_ctx *ctx);
 int p0k_device_info_get(p0k_ctx *ctx, p0k_device_info *out);
+/* Kernel choice reads the device's CU count and the P0K_* tuning switches of the environment (P0K_MFMA_TILE,
+ * P0K_MFMA_KERNEL, P0K_DMA_TAIL, P0K_GEMV_MF, P0K_GEMV_SLICES, P0K_ATTN_BQ) once, when the context is created;
+ * p0k_ctx_reload_env reads the switches again (no counterpart in the reference, whose tuning is gpu.tune,
+ * src/core/tune.js:30-36). p0k_ctx_cus: the CU count the context plans for. */
+int p0k_ctx_reload_env(p0k_ctx *ctx);
+int p0k_ctx_cus(p0k_ctx *ctx);
 
 /* ---- buffers */
+/* alloc / free return P0K_E_ARG while the context's stream is being captured into a graph (a clear or a hipFree
+ * must not land in the graph). */
 int p0k_alloc(p0k_ctx *ctx, uint64_t bytes, void **out);        /* zeroed; reuses a pooled buffer of the same rounded size */
 int p0k_free(p0k_ctx *ctx, void *buf);                          /* back to the pool (or released) */
 int p0k_drain_pool(p0k_ctx *ctx);
@@ -187,7 +195,8 @@ int p0k_sync(p0k_ctx *ctx);
 int p0k_gemm_check(const p0k_gemm_args *a);                    /* validation only (no context, no GPU) */
 int p0k_gemm(p0k_ctx *ctx, const p0k_gemm_args *a);            /* validate + enqueue; returns the status */
 double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the reference's return value (gemm.js:326) */
-int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use */
+int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use (for a
+                                                                   256-CU device and the current environment) */
 int p0k_rowstats_check(const p0k_rowstats_args *a);
 int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
 

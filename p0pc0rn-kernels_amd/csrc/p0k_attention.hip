@@ -244,11 +244,8 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
   }
 }
 
-int attention_bq(uint32_t Lq, uint32_t Hq, int cus) {
-  if (const char *ov = getenv("P0K_ATTN_BQ")) {                 // tuning / tests: force 128 or 256
-    const int v = atoi(ov);
-    if (v == 128 || v == 256) return v;
-  }
+int attention_bq(uint32_t Lq, uint32_t Hq, int cus, int force) {
+  if (force == 128 || force == 256) return force;                 // tuning / tests (P0K_ATTN_BQ)
   // 128 (two workgroups per CU). 256 queries per workgroup halve the LDS fill per query but run one workgroup per CU:
   // 24 heads x 4096 queries, 300 us vs 280 us (its 384 blocks leave half the CUs idle in the second round, where
   // the 768 blocks of 128 let the last third of a CU's blocks run alone and faster)
@@ -258,9 +255,9 @@ int attention_bq(uint32_t Lq, uint32_t Hq, int cus) {
   return 128;
 }
 
-hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s) {
+hipError_t launch_attention(const AttnParams &p, int cus, int force_bq, hipStream_t s) {
   if (p.Lq == 0 || p.Hq == 0) return hipSuccess;
-  const int bq = attention_bq(p.Lq, p.Hq, cus);
+  const int bq = attention_bq(p.Lq, p.Hq, cus, force_bq);
   dim3 grid(((p.Lq + bq - 1) / bq) * p.Hq);
   if (bq == 256) {
     if (p.cap > 0.0f) hipLaunchKernelGGL((k_attention<256, true>), grid, dim3(512), 0, s, p);

@@ -5,6 +5,7 @@
 // missing binding (:313). Those messages are kept. The reference binds whole WebGPU buffers and relies on robust buffer
 // access; a HIP kernel has none, so this build also refuses any call whose reads or writes leave the given buffer sizes,
 // and any alignment the 128-bit loads cannot honour (the reference's vec4 views need the same alignments, gemm.js:43-46).
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -49,7 +50,28 @@ static const char *epi_name(int e) {
 // size of [off, end) available in a (buf, off, size) operand
 static uint64_t avail(uint64_t size, uint64_t off) { return size > off ? size - off : 0; }
 
-int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err) {
+Tuning tuning_from_env(unsigned cus) {
+  Tuning t;
+  t.cus = cus ? cus : 256;
+  if (const char *ov = getenv("P0K_GEMV_MF")) t.gemv_mf = atoi(ov) != 0;
+  if (const char *ov = getenv("P0K_GEMV_SLICES")) t.gemv_slices = (unsigned)std::max(0, atoi(ov));
+  if (const char *ov = getenv("P0K_MFMA_KERNEL")) t.mfma_reg = strcmp(ov, "reg") == 0;
+  if (const char *ov = getenv("P0K_MFMA_TILE")) {
+    unsigned tm = 0, tn = 0;
+    if (sscanf(ov, "%ux%u", &tm, &tn) == 2 && (tm == 128 || tm == 256) && (tn == 128 || tn == 256)) {
+      t.tile_m = tm;
+      t.tile_n = tn;
+    }
+  }
+  if (const char *ov = getenv("P0K_DMA_TAIL")) t.dma_tail = atoi(ov) != 0;
+  if (const char *ov = getenv("P0K_ATTN_BQ")) {
+    const int v = atoi(ov);
+    if (v == 128 || v == 256) t.attn_bq = v;
+  }
+  return t;
+}
+
+int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err, const Tuning &tune) {
   NEED(a != nullptr, "gemm: no arguments");
   NEED(a->struct_size == sizeof(p0k_gemm_args), "gemm: struct_size %u, this library expects %u (ABI %d)", a->struct_size,
        (unsigned)sizeof(p0k_gemm_args), P0K_ABI_VERSION);
@@ -235,12 +257,12 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // f16 at any M <= 16: the matrix cores (the VALU stream's work grows with M: 31 vs 22 us at M = 4; and for q8 /
       // f16 its per-lane loads read 16 of every 64 bytes per load: q8 2.8 vs 3.6 TB/s, f16 1.4 vs 3.7)
       bool mf = M >= 3 || we != P0K_ENC_Q4G32A_T64;
-      if (const char *ov = getenv("P0K_GEMV_MF")) mf = mf && atoi(ov) != 0;   // tuning: the VALU stream for M > 1
-      gemv_split(p, we, MI355X_CUS, mf, &S, &KS);
+      if (tune.gemv_mf >= 0) mf = mf && tune.gemv_mf != 0;   // tuning: the VALU stream for M > 1
+      gemv_split(p, we, tune.cus, mf, &S, &KS);
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
-      if (const char *ov = getenv("P0K_GEMV_SLICES")) {
-        unsigned s2 = (unsigned)atoi(ov), quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
-        if (s2 && K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, mf)) { S = s2; KS = K / s2; }
+      if (tune.gemv_slices) {
+        unsigned s2 = tune.gemv_slices, quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
+        if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, mf)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
     }
@@ -249,21 +271,13 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   if (plan) {
     plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128;
     // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
-    if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes)) {
-      const char *ov = getenv("P0K_MFMA_KERNEL");
-      if (!ov || strcmp(ov, "reg") != 0) kernel = plan->kernel = K_MFMA_DMA;
-    }
-    if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, MI355X_CUS, &plan->bm, &plan->bn);
-    if (kernel == K_MFMA) mfma_tile(M, N, MI355X_CUS, &plan->bm, &plan->bn);
-    if (kernel == K_MFMA || kernel == K_MFMA_DMA) {
+    if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes) && !tune.mfma_reg) kernel = plan->kernel = K_MFMA_DMA;
+    if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, tune.cus, &plan->bm, &plan->bn);
+    if (kernel == K_MFMA) mfma_tile(M, N, tune.cus, &plan->bm, &plan->bn);
+    if ((kernel == K_MFMA || kernel == K_MFMA_DMA) && tune.tile_m) {
       // tuning / test override of the tile (P0K_MFMA_TILE=256x128); results do not depend on it
-      if (const char *ov = getenv("P0K_MFMA_TILE")) {
-        unsigned tm = 0, tn = 0;
-        if (sscanf(ov, "%ux%u", &tm, &tn) == 2 && (tm == 128 || tm == 256) && (tn == 128 || tn == 256)) {
-          plan->bm = tm;
-          plan->bn = tn;
-        }
-      }
+      plan->bm = tune.tile_m;
+      plan->bn = tune.tile_n;
     }
     plan->S = S; plan->KS = KS;
   }

@@ -464,14 +464,14 @@ hipError_t launch_dma_one(const Params &p, hipStream_t s) {
 }
 
 template <int WE, int XG>
-hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, hipStream_t s) {
+hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, unsigned cus, hipStream_t s) {
   if (bm == 256 && bn == 256) return launch_dma_one<WE, XG, 256, 256, 8>(p, s);
   if (bm == 256 && bn == 128) {
     // 8 waves (2 x 4, 128 x 32 each), one workgroup per CU; q4, whose 4-wave form fits two workgroups per CU, keeps
-    // that when the grid holds more than one tile per CU
+    // that when the grid holds more than one tile per CU (the same dma_wgs the planner scored the tile with)
     if constexpr (WE == W_Q4) {
       const uint64_t tiles = (uint64_t)((p.M + 255) / 256) * ((p.N - p.nbase + 127) / 128);
-      if (tiles > MI355X_CUS) return launch_dma_one<WE, XG, 256, 128, 4>(p, s);
+      if (dma_wgs(WE, 256, 128, tiles, cus) > 1) return launch_dma_one<WE, XG, 256, 128, 4>(p, s);
     }
     return launch_dma_one<WE, XG, 256, 128, 8>(p, s);
   }
@@ -545,7 +545,7 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 // The tile: each candidate scored by its relative per-CU rate times the fraction of workgroup slots (one or two per
 // CU, as the tile's LDS allows) that hold real work over the rounds the grid needs.
 // workgroups per CU of a tile for a grid of `tiles` (q4 256 x 128: 8 waves when the grid has one tile per CU at most)
-static unsigned dma_wgs(int we, unsigned m, unsigned n, uint64_t tiles, unsigned cus) {
+unsigned dma_wgs(int we, unsigned m, unsigned n, uint64_t tiles, unsigned cus) {
   if (m == 256 && n == 256) return 1;
   if (m == 256 && (we != W_Q4 || tiles <= cus)) return 1;           // 8 waves
   if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
@@ -584,11 +584,11 @@ void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm
   }
 }
 
-static hipError_t launch_dma_x(const Params &p, int we, unsigned bm, unsigned bn, hipStream_t s) {
+static hipError_t launch_dma_x(const Params &p, int we, unsigned bm, unsigned bn, unsigned cus, hipStream_t s) {
   switch (we) {
-  case W_Q4: return launch_dma_we<W_Q4, X_F16>(p, bm, bn, s);
-  case W_Q8: return launch_dma_we<W_Q8, X_F16>(p, bm, bn, s);
-  case W_F16: return launch_dma_we<W_F16, X_F16>(p, bm, bn, s);
+  case W_Q4: return launch_dma_we<W_Q4, X_F16>(p, bm, bn, cus, s);
+  case W_Q8: return launch_dma_we<W_Q8, X_F16>(p, bm, bn, cus, s);
+  case W_F16: return launch_dma_we<W_F16, X_F16>(p, bm, bn, cus, s);
   }
   return hipErrorInvalidValue;
 }
@@ -603,8 +603,6 @@ void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned
   *ncut = N;
   *bm2 = bm;
   *bn2 = bn;
-  if (const char *ov = getenv("P0K_DMA_TAIL"))
-    if (atoi(ov) == 0) return;
   const uint32_t tilesM = (M + bm - 1) / bm, tilesN = (N + bn - 1) / bn, T = tilesM * tilesN;
   const uint32_t slots = cus * dma_wgs(we, bm, bn, T, cus), full = T / slots * slots, tail = T - full;
   if (tail == 0 || 2 * tail > slots || full < tilesM) return;
@@ -614,25 +612,26 @@ void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned
   dma_tile(M, N - *ncut, we, X_F16, cus, bm2, bn2);
 }
 
-hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s) {
+hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, unsigned cus, bool tail,
+                           hipStream_t s) {
   if (xg != X_CONV3) {
-    uint32_t ncut;
-    unsigned bm2, bn2;
-    dma_tail(p.M, p.N, we, bm, bn, MI355X_CUS, &ncut, &bm2, &bn2);
-    if (ncut >= p.N) return launch_dma_x(p, we, bm, bn, s);
+    uint32_t ncut = p.N;
+    unsigned bm2 = bm, bn2 = bn;
+    if (tail) dma_tail(p.M, p.N, we, bm, bn, cus, &ncut, &bm2, &bn2);
+    if (ncut >= p.N) return launch_dma_x(p, we, bm, bn, cus, s);
     Params a = p, b = p;
     a.N = ncut;                                                 // epilogue bounds: the first launch's columns only
     a.nbase = 0;
     b.nbase = ncut;
-    hipError_t e = launch_dma_x(a, we, bm, bn, s);
+    hipError_t e = launch_dma_x(a, we, bm, bn, cus, s);
     if (e != hipSuccess) return e;
-    return launch_dma_x(b, we, bm2, bn2, s);
+    return launch_dma_x(b, we, bm2, bn2, cus, s);
   }
   if (xg == X_CONV3) {
     switch (we) {
-    case W_Q4: return launch_dma_we<W_Q4, X_CONV3>(p, bm, bn, s);
-    case W_Q8: return launch_dma_we<W_Q8, X_CONV3>(p, bm, bn, s);
-    case W_F16: return launch_dma_we<W_F16, X_CONV3>(p, bm, bn, s);
+    case W_Q4: return launch_dma_we<W_Q4, X_CONV3>(p, bm, bn, cus, s);
+    case W_Q8: return launch_dma_we<W_Q8, X_CONV3>(p, bm, bn, cus, s);
+    case W_F16: return launch_dma_we<W_F16, X_CONV3>(p, bm, bn, cus, s);
     }
     return hipErrorInvalidValue;
   }

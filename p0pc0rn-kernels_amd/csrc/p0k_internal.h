@@ -9,8 +9,21 @@ struct Params;
 enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2, K_MFMA_DMA = 3 };
 // kernel choice of one call: GEMV items are (128-column tile) x (K slice of KS), S slices per tile
 struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; };
+// What the kernel choice depends on besides the call: the device's CU count and the P0K_* tuning switches of the
+// environment. A context reads them once (at creation and on p0k_ctx_reload_env); calls without a context read
+// them on the spot.
+struct Tuning {
+  unsigned cus = 256;
+  int gemv_mf = -1;            // P0K_GEMV_MF=0: the VALU stream for M > 1 (-1: not set)
+  unsigned gemv_slices = 0;    // P0K_GEMV_SLICES=n: decode K slices (0: not set)
+  bool mfma_reg = false;       // P0K_MFMA_KERNEL=reg: the register-staged MFMA kernel
+  unsigned tile_m = 0, tile_n = 0;   // P0K_MFMA_TILE=MxN
+  bool dma_tail = true;        // P0K_DMA_TAIL=0: one launch for a mostly empty last round
+  int attn_bq = 0;             // P0K_ATTN_BQ=128|256
+};
+Tuning tuning_from_env(unsigned cus);
 // validate a gemm call and translate it to kernel parameters (device pointers are filled in by the caller)
-int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err);
+int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err, const Tuning &t);
 int prepare_rowstats(const p0k_rowstats_args *a, std::string *err);
 int prepare_pixstats(const p0k_pixstats_args *a, std::string *err);
 struct AttnParams;

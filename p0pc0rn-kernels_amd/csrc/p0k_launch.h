@@ -6,7 +6,6 @@
 namespace p0k {
 struct Params;
 constexpr int GEMV_MAX_M = 16;
-constexpr unsigned MI355X_CUS = 256;
 // MFMA GEMM (any M): bm x bn tiles in {128, 256}^2, 512 threads; mfma_tile picks the tile for a shape
 void mfma_tile(uint32_t M, uint32_t N, unsigned cus, unsigned *bm, unsigned *bn);
 hipError_t launch_gemm_mfma(const Params &p, int we, int xm, unsigned bm, unsigned bn, hipStream_t s);
@@ -20,8 +19,12 @@ void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm
 // rest with bm2 x bn2 (ncut == N: one launch)
 void dma_tail(uint32_t M, uint32_t N, int we, unsigned bm, unsigned bn, unsigned cus, uint32_t *ncut, unsigned *bm2,
               unsigned *bn2);
+// workgroups per CU of a tile for a grid of `tiles` (q4 256 x 128: 8 waves, one per CU, when the grid has at most one
+// tile per CU; 4 waves, two per CU, otherwise): the planner scores tiles with it and the launcher picks the wave count
+unsigned dma_wgs(int we, unsigned m, unsigned n, uint64_t tiles, unsigned cus);
 hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s);
-hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, hipStream_t s);
+// cus: the device's CU count; tail: allow the column split of dma_tail
+hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigned bn, unsigned cus, bool tail, hipStream_t s);
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
 // (part: S*M*N floats, cnt: one zeroed counter per 128-column tile). mf: the matrix-core variant (2 <= M <= 16).
 void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S, unsigned *KS);
@@ -38,8 +41,8 @@ struct AttnParams {
   uint32_t Lq, Lk, ldo, Hq, Hkv, mode, nvalid;
   float scale, cap;            // natural-log scale; cap > 0: scores -> cap * tanh(scores / cap)
 };
-int attention_bq(uint32_t Lq, uint32_t Hq, int cus);   // queries per workgroup
-hipError_t launch_attention(const AttnParams &p, int cus, hipStream_t s);
+int attention_bq(uint32_t Lq, uint32_t Hq, int cus, int force);   // queries per workgroup (force: 128 / 256 or 0)
+hipError_t launch_attention(const AttnParams &p, int cus, int force_bq, hipStream_t s);
 // pixstats and GroupNorm statistics (src/ops/video.js:301-321, src/ops/misc.js:50-109)
 hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, float *r, hipStream_t s);
 hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);

@@ -61,6 +61,11 @@ struct p0k_ctx {
   uint64_t ws_x_bytes = 0;
   // 256 zero bytes: the padding taps of the load-to-LDS conv3 gather read them
   void *ws_zero = nullptr;
+  // workspaces replaced by larger ones: a graph captured earlier may still address them, so they are freed only
+  // with the context
+  std::vector<void *> ws_retired;
+  // CU count of the device and the P0K_* tuning switches, read at creation and by p0k_ctx_reload_env
+  p0k::Tuning tune;
 };
 
 struct p0k_event { hipEvent_t ev; int device; };
@@ -83,6 +88,7 @@ int p0k_ctx_create(int device, p0k_ctx **out) {
     return set_err(P0K_E_UNSUPPORTED, std::string("ctx_create: this library is built for gfx950, the device is ") + prop.gcnArchName);
   p0k_ctx *c = new p0k_ctx();
   c->device = device;
+  c->tune = p0k::tuning_from_env((unsigned)prop.multiProcessorCount);
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) { delete c; return hip_err(e, "hipStreamCreate"); }
   e = hipMalloc((void **)&c->ws_cnt, sizeof(uint32_t) * p0k_ctx::WS_COUNTERS);
@@ -111,9 +117,19 @@ void p0k_ctx_destroy(p0k_ctx *c) {
   if (c->ws_x) (void)hipFree(c->ws_x);
   if (c->ws_zero) (void)hipFree(c->ws_zero);
   if (c->ws_cnt) (void)hipFree(c->ws_cnt);
+  for (void *p : c->ws_retired) (void)hipFree(p);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
+
+int p0k_ctx_reload_env(p0k_ctx *c) {
+  if (!c) return set_err(P0K_E_ARG, "ctx_reload_env: NULL context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->tune = p0k::tuning_from_env(c->tune.cus);
+  return P0K_OK;
+}
+
+int p0k_ctx_cus(p0k_ctx *c) { return c ? (int)c->tune.cus : 0; }
 
 int p0k_device_info_get(p0k_ctx *c, p0k_device_info *out) {
   if (!c || !out) return set_err(P0K_E_ARG, "device_info: NULL argument");
@@ -150,10 +166,21 @@ static void evict(p0k_ctx *c, uint64_t room) {     // release pooled buffers, ol
   }
 }
 
+// alloc / free queue a clear or call hipFree: neither belongs in a graph being captured on the context's stream
+static int refuse_capture(p0k_ctx *c, const char *what) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return set_err(P0K_E_ARG, std::string(what) + ": not allowed while the context's stream is captured into a graph "
+                                                  "(allocate and free buffers before p0k_graph_begin or after p0k_graph_end)");
+  return P0K_OK;
+}
+
 int p0k_alloc(p0k_ctx *c, uint64_t bytes, void **out) {
   if (!c || !out) return set_err(P0K_E_ARG, "alloc: NULL argument");
   *out = nullptr;
   std::lock_guard<std::mutex> lk(c->mu);
+  if (int r = refuse_capture(c, "alloc")) return r;
   uint64_t size = std::max<uint64_t>(16, (bytes + 15) / 16 * 16);
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
   auto it = c->pool.find(size);
@@ -189,6 +216,7 @@ int p0k_free(p0k_ctx *c, void *p) {
   if (!c) return set_err(P0K_E_ARG, "free: NULL context");
   if (!p) return P0K_OK;
   std::lock_guard<std::mutex> lk(c->mu);
+  if (int r = refuse_capture(c, "free")) return r;
   auto it = c->live.find(p);
   if (it == c->live.end()) return set_err(P0K_E_ARG, "free: not a live buffer of this context");
   uint64_t size = it->second;
@@ -280,7 +308,7 @@ int p0k_sync(p0k_ctx *c) {
 // ------------------------------------------------------------------------------------------------ the op
 int p0k_gemm_check(const p0k_gemm_args *a) {
   std::string err;
-  int r = p0k::prepare_gemm(a, nullptr, nullptr, &err);
+  int r = p0k::prepare_gemm(a, nullptr, nullptr, &err, p0k::tuning_from_env(256));
   if (r) return set_err(r, err);
   return P0K_OK;
 }
@@ -290,7 +318,7 @@ double p0k_gemm_flops(const p0k_gemm_args *a) { return a ? 2.0 * a->M * a->N * a
 int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out) {
   std::string err;
   p0k::Plan plan;
-  int r = p0k::prepare_gemm(a, nullptr, &plan, &err);
+  int r = p0k::prepare_gemm(a, nullptr, &plan, &err, p0k::tuning_from_env(256));
   if (r) return set_err(r, err);
   if (out) { out->bm = plan.bm; out->bn = plan.bn; out->kernel = plan.kernel; }
   return P0K_OK;
@@ -316,12 +344,13 @@ static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t need, const
   if (cs != hipStreamCaptureStatusNone)
     return set_err(P0K_E_ARG, std::string("gemm: the ") + what + " workspace must grow (" + std::to_string(need) +
                                   " bytes): make one call of this shape before capturing a graph");
-  HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-  if (*buf) HIPCHK(hipFree(*buf), "hipFree");
-  *buf = nullptr;
-  *bytes = 0;
-  hipError_t me = hipMalloc(buf, need);
+  void *nb = nullptr;
+  hipError_t me = hipMalloc(&nb, need);
   if (me != hipSuccess) return set_err(P0K_E_NOMEM, std::string("gemm: ") + what + " workspace of " + std::to_string(need) + " bytes");
+  // the old workspace stays allocated until the context is destroyed: a graph captured before this call still
+  // addresses it, and replaying that graph must not touch freed memory
+  if (*buf) c->ws_retired.push_back(*buf);
+  *buf = nb;
   *bytes = need;
   return P0K_OK;
 }
@@ -331,7 +360,12 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   std::string err;
   p0k::Params p;
   p0k::Plan plan;
-  int r = p0k::prepare_gemm(a, &p, &plan, &err);
+  p0k::Tuning tune;
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    tune = c->tune;
+  }
+  int r = p0k::prepare_gemm(a, &p, &plan, &err, tune);
   if (r) return set_err(r, err);
   {
     std::lock_guard<std::mutex> lk(c->mu);
@@ -368,7 +402,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
       if (e != hipSuccess) return hip_err(e, "gemm prologue launch");
       p.X = (const uint8_t *)c->ws_x;
     }
-    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_CONV3, plan.bm, plan.bn, c->stream);
+    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_CONV3, plan.bm, plan.bn, tune.cus, false, c->stream);
   } else if (plan.kernel == p0k::K_MFMA_DMA) {
     if (plan.xm != P0K_X_F16) {
       // the prologue once per element into the X' workspace; the GEMM then reads fp16 rows
@@ -380,7 +414,7 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
       p.ldx = a->K;
       p.kx0 = 0;
     }
-    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_F16, plan.bm, plan.bn, c->stream);
+    e = p0k::launch_gemm_dma(p, plan.we, P0K_X_F16, plan.bm, plan.bn, tune.cus, tune.dma_tail, c->stream);
   } else {
     e = p0k::launch_gemm_mfma(p, plan.we, plan.xm, plan.bm, plan.bn, c->stream);
   }
@@ -459,7 +493,7 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
       (r = check_live(c, a->v_buf, a->v_size, "attention", "v")) || (r = check_live(c, a->o_buf, a->o_size, "attention", "o")))
     return r;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_attention(p, p0k::MI355X_CUS, c->stream);
+  hipError_t e = p0k::launch_attention(p, (int)c->tune.cus, c->tune.attn_bq, c->stream);
   if (e != hipSuccess) return hip_err(e, "attention launch");
   return P0K_OK;
 }

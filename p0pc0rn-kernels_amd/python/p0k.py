@@ -130,6 +130,7 @@ class DeviceInfo(C.Structure):
 
 EXPORTS = [
     "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
+    "p0k_ctx_reload_env", "p0k_ctx_cus",
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
     "p0k_attention_check", "p0k_attention", "p0k_attention_flops",
@@ -153,6 +154,7 @@ def lib():
         sigs = {
             "p0k_abi_version": ([], I), "p0k_last_error": ([], C.c_char_p),
             "p0k_ctx_create": ([I, C.POINTER(P)], I), "p0k_ctx_destroy": ([P], None),
+            "p0k_ctx_reload_env": ([P], I), "p0k_ctx_cus": ([P], I),
             "p0k_device_info_get": ([P, C.POINTER(DeviceInfo)], I),
             "p0k_alloc": ([P, U64, C.POINTER(P)], I), "p0k_free": ([P, P], I), "p0k_drain_pool": ([P], I),
             "p0k_pool_stats_get": ([P, C.POINTER(PoolStats)], I),
@@ -278,6 +280,13 @@ class Buffer:
         self.ptr, self.size, self.dev = ptr, size, dev
 
 
+TUNING_SWITCHES = ("P0K_MFMA_TILE", "P0K_MFMA_KERNEL", "P0K_DMA_TAIL", "P0K_GEMV_MF", "P0K_GEMV_SLICES", "P0K_ATTN_BQ")
+
+
+def _tuning_env():
+    return tuple(os.environ.get(k) for k in TUNING_SWITCHES)
+
+
 class Device:
     """createGpu() over libp0k: one HIP device, one stream."""
 
@@ -286,11 +295,23 @@ class Device:
         ctx = C.c_void_p()
         _chk(L.p0k_ctx_create(device, C.byref(ctx)))
         self.ctx = ctx
+        self._env = _tuning_env()
+
+    def _sync_env(self):
+        """the context reads the P0K_* tuning switches once; read them again when this process has changed them"""
+        env = _tuning_env()
+        if env != self._env:
+            _chk(lib().p0k_ctx_reload_env(self.ctx))
+            self._env = env
 
     def close(self):
         if self.ctx:
             lib().p0k_ctx_destroy(self.ctx)
             self.ctx = None
+
+    def cus(self):
+        """the CU count the context plans tiles and splits for (the device's, not a constant)"""
+        return lib().p0k_ctx_cus(self.ctx)
 
     def info(self):
         d = DeviceInfo()
@@ -342,6 +363,7 @@ class Device:
     def gemm(self, a):
         """gemm(gpu, args) of src/ops/gemm.js:268: validate, enqueue, return the FLOPs (2MNK)."""
         s = gemm_args(a, self.resolve)
+        self._sync_env()
         _chk(lib().p0k_gemm(self.ctx, C.byref(s)))
         return 2 * a["M"] * a["N"] * a["K"]
 
@@ -363,6 +385,7 @@ class Device:
     def attention(self, a):
         """attention(gpu, a) of src/ops/attention.js:168 (head size 128); returns 4 Lq Lk 128 Hq."""
         s = attn_args(a, self.resolve)
+        self._sync_env()
         _chk(lib().p0k_attention(self.ctx, C.byref(s)))
         return lib().p0k_attention_flops(C.byref(s))
 

@@ -92,9 +92,10 @@ class Case:
 
 def make_case(enc="f16", xmode="f16", epi="f16", M=32, N=128, K=256, seed=1, wscale=0.05, *, act="silu", bias=False,
               gate=False, store=False, res=False, rope_mode=None, Hq=None, Hkv=None, Ltot=None, row_off=0,
-              ld_pad=0, k0=0, n0=0, wk0=0, wr0=0, x_uniform=False, tile=None, eps=1e-6, acc=None):
+              ld_pad=0, k0=0, n0=0, wk0=0, wr0=0, x_uniform=False, tile=None, eps=1e-6, acc=None, rope_grid_w=None):
     """A seeded case of any (encoding, prologue, epilogue). Shapes: ws columns N; for swiglu the weight holds
-    [gate N/2 | up N/2] rows (wr0 = 0, wr1 = N/2); for heads N = (Hq + 2 Hkv) * 128."""
+    [gate N/2 | up N/2] rows (wr0 = 0, wr1 = N/2); for heads N = (Hq + 2 Hkv) * 128, with a 1-D RoPE table, or the
+    2-D table of a token grid rope_grid_w wide."""
     bufs, spec = {}, {}
     glu = epi == "swiglu"
     Kt = K + wk0
@@ -144,7 +145,7 @@ def make_case(enc="f16", xmode="f16", epi="f16", M=32, N=128, K=256, seed=1, wsc
         assert N == (Hq + 2 * Hkv) * 128
         Ltot = Ltot or (row_off + M)
         bufs["y"] = np.zeros((Hq + 2 * Hkv) * Ltot * 128, np.uint16)
-        bufs["rope"] = rope_table_1d(Ltot)
+        bufs["rope"] = rope_table_2d(Ltot, rope_grid_w) if rope_grid_w else rope_table_1d(Ltot)
         bufs["ev"] = (1.0 + oracle.randn(256, seed * 7 + 5, 0.1)).astype(np.float32)
         spec["ev"] = {"buf": "ev", "off": 0}
         spec["heads"] = {"Ltot": Ltot, "Hq": Hq, "Hkv": Hkv, "rowOff": row_off, "eps": eps,

@@ -182,3 +182,27 @@ def test_conv3_gather_tile_choice():
     t = p0k.select_tile(host_args(make_conv3_case(T=13, H=92, W=160, C=128, N=128)))
     assert t["kernel"] == "mfma_dma" and (t["BM"], t["BN"]) == (256, 128)
     assert p0k.select_tile(host_args(make_conv3_case(T=4, H=6, W=8, C=32, N=128)))["kernel"] == "mfma"
+
+
+def test_tuning_switches_read_per_call_without_a_context(monkeypatch):
+    """p0k_select_tile (no context) reads the P0K_* switches when called; a context reads them once and again on
+    p0k_ctx_reload_env (the Python Device does that when this process changed them)."""
+    a = host_args(make_case(enc="q4g32a.t64", M=2048, N=4096, K=64))
+    base = p0k.select_tile(a)
+    monkeypatch.setenv("P0K_MFMA_TILE", "128x128")
+    t = p0k.select_tile(a)
+    assert (t["BM"], t["BN"]) == (128, 128)
+    monkeypatch.setenv("P0K_MFMA_TILE", "100x7")                  # not a tile: ignored
+    assert p0k.select_tile(a) == base
+    monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
+    assert p0k.select_tile(a)["kernel"] == "mfma"
+    monkeypatch.delenv("P0K_MFMA_KERNEL")
+    monkeypatch.delenv("P0K_MFMA_TILE")
+    assert p0k.select_tile(a) == base
+
+
+def test_null_context_calls_are_refused():
+    L = p0k.lib()
+    assert L.p0k_ctx_reload_env(None) == p0k.E_ARG
+    assert L.p0k_ctx_cus(None) == 0
+    assert L.p0k_alloc(None, 16, C.byref(C.c_void_p())) == p0k.E_ARG

@@ -77,7 +77,7 @@ def test_decode_m1_other_weights_full(dev, enc, epi, N):
 FULL = {
     "prefill_q8_rms_resadd": dict(enc="q8g64s.t64", xmode="rms", epi="resadd", M=2048, N=4096, K=4096, wscale=0.02),
     "dit_qkv_q4_lnmod_heads": dict(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=4096, N=9216, K=3072, Hq=24,
-                                   Hkv=24, wscale=0.02),
+                                   Hkv=24, wscale=0.02, rope_grid_w=64),
     "dit_up_q4_geglu": dict(enc="q4g32a.t64", epi="swiglu", act="gelu", M=4096, N=24576, K=3072, wscale=0.02),
     "prefill_q8_rms_bias_f16res": dict(enc="q8g64s.t64", xmode="rms", epi="bias", res=True, M=2048, N=4096, K=4096,
                                        wscale=0.02),
@@ -99,8 +99,10 @@ def test_prefill_full(dev, name):
 
 def test_conv3_full_clip(dev):
     """3x3x3 conv 128 -> 128 over 13 x 92 x 160: sampled image rows of frames 0, 6 and 12 against the
-    oracle (the first and last frames read the zero padding in time), then 4-frame ring calls (each output frame t
-    from a ring holding t - 1 .. t + 1) bit-identical to the whole clip."""
+    oracle (the first and last frames repeat themselves in time: the input frame index is clamped to the clip, as in
+    test/kernels.test.js:56), then 4-frame ring calls (each output frame t from a ring holding t - 1 .. t + 1) and
+    linear chunks of two output frames per call (padT = t0, the chunk's input starting at frame padL = max(0, t0 - 1))
+    bit-identical to the whole clip."""
     T, H, W, C, N = 13, 92, 160, 128, 128
     banner("full-size conv3")
     c = make_conv3_case(T, H, W, C, N, seed=103, wscale=0.02)
@@ -120,6 +122,15 @@ def test_conv3_full_clip(dev):
             _conv3_call(dev, c, dw, ring, 0, yb, t * fy, t, 1, 0, 4)
             dev.done()
         assert np.array_equal(dev.read(yb, np.uint16, T * H * W * N), whole), "4-frame ring differs from the whole clip"
+        # linear chunks: output frames t0, t0 + 1 from input frames padL .. t0 + 2, the chunk's start given by padL
+        yc = dev.buffer(T * fy)
+        for t0 in range(0, T, 2):
+            padL = max(0, t0 - 1)
+            _conv3_call(dev, c, dw, dx, padL * fx, yc, t0 * fy, t0, min(2, T - t0), padL)
+        dev.done()
+        chunks = dev.read(yc, np.uint16, T * H * W * N)
+        dev.free(yc)
+        assert np.array_equal(chunks, whole), "2-frame linear chunks differ from the whole clip"
     finally:
         for b in (dw, dx, ring, yb):
             dev.free(b)

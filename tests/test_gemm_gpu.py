@@ -60,6 +60,22 @@ def test_reference_partial_tiles(dev):
     assert_close(got, c.run_oracle())
 
 
+def test_config0_plain_f16_gemm(dev):
+    """BASELINE configs[0], the reference's own correctness shape class (test/kernels.test.js:72-92) at M 64, N 256,
+    K 512: x fp16 U[-1, 1], w fp16 N(0, 0.02). The reference's bar (cos > 0.9995 against the float64 cpuGemm) and the
+    per-element tolerance against the oracle."""
+    M, N, K = 64, 256, 512
+    banner("configs[0] plain f16 GEMM")
+    c = make_case(enc="f16", M=M, N=N, K=K, seed=64, wscale=0.02, x_uniform=True)
+    X = oracle.h2f(c.bufs["x"])
+    Wd = oracle.h2f(c.bufs["w"].view(np.uint16))
+    assert X.min() >= -1.0 and X.max() <= 1.0
+    got = c.run_device(dev)
+    cos, _ = cos_maxerr(to_float(got), oracle.cpu_gemm(X, Wd, M, N, K))
+    assert cos > 0.9995
+    assert_close(got, c.run_oracle(), what="configs[0]")
+
+
 # ------------------------------------------------------------------------------------------------ all prologues/epilogues
 EPIS = [
     ("f16", "f16", {}),
@@ -352,3 +368,81 @@ def test_conv3_every_mfma_tile_bit_identical(dev, t, monkeypatch):
     got = c.run_device(dev)
     assert np.array_equal(got, base)
     assert_close(got, c.run_oracle(), what=f"conv3 tile {t}")
+
+
+def test_q4_256x128_four_wave_grid(dev, monkeypatch):
+    """q4 256 x 128 tiles run with 8 waves when the grid holds at most one tile per CU and with 4 waves (two
+    workgroups per CU) otherwise. 4096 x 4352 gives 16 x 34 = 544 tiles, so the forced 256 x 128 tile takes the
+    4-wave kernel: sampled rows match the oracle and the result is bit-identical to the 256 x 256 tile's."""
+    kw = dict(enc="q4g32a.t64", epi="f16", M=4096, N=4352, K=128)
+    c = make_case(seed=26, **kw)
+    banner(f"q4 256x128 4-wave {kw}")
+    monkeypatch.setenv("P0K_DMA_TAIL", "0")
+    outs = {}
+    for t in ("256x128", "256x256"):
+        monkeypatch.setenv("P0K_MFMA_TILE", t)
+        sel = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+        assert sel["kernel"] == "mfma_dma" and sel["BM"] == 256 and sel["BN"] == int(t.split("x")[1])
+        outs[t] = c.run_device(dev)
+    assert np.array_equal(outs["256x128"], outs["256x256"])
+    g = outs["256x128"].reshape(kw["M"], -1)
+    for m0, m1 in [(0, 8), (2050, 2058), (4088, 4096)]:
+        w = c.run_oracle(m0, m1).reshape(kw["M"], -1)
+        assert_close(g[m0:m1], w[m0:m1], what=f"rows {m0}..{m1}")
+
+
+# ------------------------------------------------------------------------------------------------ runtime robustness
+def test_context_plans_for_the_device_cu_count(dev):
+    assert dev.cus() == dev.info()["cus"] > 0
+
+
+def test_alloc_and_free_refused_while_capturing(dev):
+    """a buffer clear or hipFree must not land in a captured graph: alloc / free are refused during capture"""
+    b = dev.buffer(256)
+    dev.graph_begin()
+    try:
+        with pytest.raises(p0k.P0kError, match="captured into a graph"):
+            dev.buffer(256)
+        with pytest.raises(p0k.P0kError, match="captured into a graph"):
+            lib_free = p0k.lib().p0k_free(dev.ctx, b.ptr)
+            p0k._chk(lib_free)
+    finally:
+        g = dev.graph_end()
+    dev.graph_destroy(g)
+    dev.free(b)
+
+
+def test_graph_survives_workspace_growth(dev):
+    """A graph captured with a split-K decode call keeps the workspace it was captured with: a later, larger eager
+    call grows the workspace (the old one stays allocated until the context goes), and replaying the graph still
+    gives the oracle's result."""
+    small = make_case(enc="q4g32a.t64", epi="swiglu", M=1, N=1024, K=4096, seed=71, wscale=0.02)
+    big = make_case(enc="q4g32a.t64", epi="swiglu", M=8, N=8192, K=4096, seed=72, wscale=0.02)
+    for c in (small, big):
+        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"].startswith("gemv")
+    d = {k: dev.upload(v) for k, v in small.bufs.items()}
+    db = {k: dev.upload(v) for k, v in big.bufs.items()}
+    try:
+        a = small.args(lambda n: d[n])
+        dev.gemm(a)                                   # sizes the workspace for the small call
+        dev.done()
+        dev.graph_begin()
+        try:
+            dev.gemm(a)
+        finally:
+            g = dev.graph_end()
+        dev.gemm(big.args(lambda n: db[n]))           # larger: grows the workspace
+        dev.done()
+        zero = np.zeros_like(small.bufs["y"])
+        dev.upload(zero, d["y"])
+        for _ in range(3):
+            dev.graph_launch(g)
+            dev.done()
+            got = dev.read(d["y"], np.uint16, small.bufs["y"].size)
+            assert_close(got, small.run_oracle(weights=oracle.CPU_WEIGHTS), what="graph replay after growth")
+        dev.graph_destroy(g)
+        assert_close(dev.read(db["y"], np.uint16, big.bufs["y"].size), big.run_oracle(weights=oracle.CPU_WEIGHTS),
+                     what="larger eager call")
+    finally:
+        for b in list(d.values()) + list(db.values()):
+            dev.free(b)
