@@ -226,6 +226,16 @@ __device__ __forceinline__ void store_f16x8(uint8_t *yb, size_t idx, const float
   }
 }
 
+// the GLU activation of gemm.js:205-209: SiLU g / (1 + e^-g), or tanh-GELU with its argument clamped to +-15
+__device__ __forceinline__ float glu_act(float gt, bool gelu) {
+  if (gelu) {
+    float z = 0.7978845608f * (gt + 0.044715f * gt * gt * gt);
+    z = fminf(fmaxf(z, -15.0f), 15.0f);
+    return gt * 0.5f * (1.0f + tanhf(z));
+  }
+  return gt / (1.0f + __expf(-gt));
+}
+
 // sum over the 16 lanes of an aligned lane group (the 16 threads that share one row in the epilogue)
 __device__ __forceinline__ float sum16(float v) {
 #pragma unroll
@@ -255,15 +265,7 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
       for (int j = 0; j < 8; j++) {
         float gt = src[2 * j], u = src[2 * j + 1];
         if (bias && o + j < Nout) { gt += p.BV[p.bvOff + o + j]; u += p.BV[p.bvOff + p.bvUp + o + j]; }
-        float act;
-        if (gelu) {
-          float z = 0.7978845608f * (gt + 0.044715f * gt * gt * gt);
-          z = fminf(fmaxf(z, -15.0f), 15.0f);
-          act = gt * 0.5f * (1.0f + tanhf(z));
-        } else {
-          act = gt / (1.0f + __expf(-gt));
-        }
-        v[j] = act * u;
+        v[j] = glu_act(gt, gelu) * u;
       }
       store_f16x8(p.Y, (size_t)m * p.ldy + p.ny0 + o, v, Nout - o);
     }

@@ -42,7 +42,7 @@ constexpr int GV_LDS = P0K_GV_LDS_KB * 1024;                       // X' of the 
 template <int WE>
 struct Unit;
 template <>
-struct Unit<W_Q4> { static constexpr int UK = 32, PF = 8; u32x4 code; uint32_t sm; };
+struct Unit<W_Q4> { static constexpr int UK = 32, PF = 4; u32x4 code; uint32_t sm; };
 template <>
 struct Unit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x4 code[4]; uint32_t s; };
 template <>
@@ -51,6 +51,57 @@ struct Unit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
 // longest slice whose X' (2 B per k and row) and group sums (2 floats per 32 k and row) fit the LDS budget
 template <int MT>
 constexpr int ks_max() { return (GV_LDS * 8 / (MT * 18)) & ~1023; }
+
+// One call's tile without a K split, for the element-wise epilogues (f16, f32, bias, resadd, swiglu): one thread per
+// output element sums the element's K-quarters (in quarter order, as finish() does) and applies the epilogue, so the
+// tile needs no summing pass of its own and every thread has a few instructions of work (the 16-byte-store epilogue
+// of finish() gives 8 threads 8 outputs each per row, a long serial tail at the end of the stream).
+template <int MT>
+__device__ __forceinline__ void finish_fast(const Params &p, const float *sR, uint32_t nB, int tid) {
+  const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+  auto qsum = [&](uint32_t m, uint32_t c) {
+    float s = sR[m * 128 + c];
+#pragma unroll
+    for (int q = 1; q < GV_KSUB; q++) s += sR[(q * MT + m) * 128 + c];
+    return s;
+  };
+  if (p.epi == E_SWIGLU) {                                                        // gemm.js:204-210
+    const uint32_t Nout = p.N >> 1;
+    const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
+    for (uint32_t t = tid; t < rows * 64; t += GV_NT) {
+      const uint32_t m = t >> 6, c = t & 63, o = (nB >> 1) + c;
+      if (o >= Nout) continue;
+      float gt = qsum(m, 2 * c), u = qsum(m, 2 * c + 1);
+      if (bias) { gt += p.BV[p.bvOff + o]; u += p.BV[p.bvOff + p.bvUp + o]; }
+      ((uint16_t *)p.Y)[(size_t)m * p.ldy + p.ny0 + o] = h_bits(glu_act(gt, gelu) * u);
+    }
+    return;
+  }
+  for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+    const uint32_t m = t >> 7, c = t & 127, col = nB + c;
+    if (col >= p.N) continue;
+    const float v = qsum(m, c);
+    const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
+    if (p.epi == E_F16) {                                                         // gemm.js:194-196
+      ((uint16_t *)p.Y)[yi] = h_bits(v);
+    } else if (p.epi == E_F32) {
+      ((float *)p.Y)[yi] = v;
+    } else if (p.epi == E_BIAS) {                                                 // gemm.js:211-215
+      float r = v + p.EV[p.evOff + col];
+      if (p.flags & F_RES) r += h_val(((const uint16_t *)p.Y)[yi]);
+      ((uint16_t *)p.Y)[yi] = h_bits(r);
+    } else {                                                                      // resadd, gemm.js:197-203
+      const float g = (p.flags & F_GATE) ? p.EV[p.evOff + col] : 1.0f;
+      const float b = (p.flags & F_BIAS) ? p.BV[p.bvOff + col] : 0.0f;
+      float *y = (float *)p.Y + yi;
+      *y = ((p.flags & F_STORE) ? 0.0f : *y) + g * (v + b);
+    }
+  }
+}
+
+__device__ __forceinline__ bool fast_epi(const Params &p, uint32_t S) {
+  return S == 1 && p.epi != E_HEADS && p.epi != E_ONORMGATE;
+}
 
 // After the stream: the K-quarter partials of the item are in sR as [quarter][m][128 ws columns]; sum them, meet the
 // other slices of the tile when S > 1, and run the epilogue.
@@ -103,11 +154,14 @@ template <int WE, int XM, int MT>
 __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
   constexpr int UK = Unit<WE>::UK, PF = Unit<WE>::PF, KSM = ks_max<MT>(), NGM = KSM / UK;
   static_assert(GV_KSUB * MT * 128 * 4 <= GV_LDS, "partials must fit the staging buffer");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[GV_LDS];
+  // one or two rows: the partials get their own 2-4 KB, so the waves write them as they finish their streams without
+  // waiting for each other; more rows: the partials reuse the X' buffer after a barrier
+  constexpr bool SEP = MT <= 2;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GV_LDS + (SEP ? GV_KSUB * MT * 128 * 4 : 0)];
   __shared__ uint32_t sLast;
   f16 *sX = (f16 *)smem;                                       // [MT][KSM] X', pair order of the encoding
   f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [MT][KSM / UK] (Xlo, Xhi) per unit
-  float *sR = (float *)smem;                                   // after the stream: partials
+  float *sR = (float *)(smem + (SEP ? GV_LDS : 0));            // after the stream: partials
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ch = wave / GV_KSUB, sub = wave % GV_KSUB;
@@ -227,6 +281,16 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
     }
   };
 
+  // This thread's first chunk of X is loaded before the ring: loads return in issue order (one vmcnt counter per
+  // wave), so an X load issued after the ring would wait for the ring's first units and hold the staging back.
+  const uint32_t nb = KS / 8, nx = MT * nb;
+  u32x4 xv0 = (u32x4){0u, 0u, 0u, 0u};
+  {
+    const uint32_t m = (uint32_t)tid / nb;
+    if ((uint32_t)tid < nx && m < p.M) xv0 = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * ((uint32_t)tid - m * nb));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // fill the ring before X' is staged, so HBM works while the prologue runs (unconditionally, clamped to the wave's
   // last unit, in the refill order: the compiler then counts the loads in flight at the loop head exactly)
   Unit<WE> ring[PF];
@@ -236,29 +300,25 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // X' of the slice -> LDS in the pair order of the encoding; then per unit the X' sums over the low (even pair slot)
-  // and high (odd pair slot) positions
-  const uint32_t nb = KS / 8, ng = KS / UK;
-  for (uint32_t t = tid; t < MT * nb; t += GV_NT) {
-    uint32_t m = t / nb, kq = t - m * nb;
-    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-    if (m < p.M) v = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq));
+  // X' of the slice -> LDS in the pair order of the encoding, and per unit the X' sums over the low (even pair slot)
+  // and high (odd pair slot) positions: a unit's UK / 8 chunks sit in as many adjacent lanes (nx and the thread count
+  // are multiples of UK / 8, so such a lane group is active or idle as a whole), which sum across by shuffles
+  for (uint32_t t = tid; t < nx; t += GV_NT) {
+    const uint32_t m = t / nb, kq = t - m * nb;
+    u32x4 v = xv0;
+    if (t != (uint32_t)tid) v = m < p.M ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq) : (u32x4){0u, 0u, 0u, 0u};
+    v = xperm<WE>(v);
     *(u32x4 *)(sX + m * KSM + 8 * kq) = v;
-  }
-  if constexpr (WE != W_F16) {
-    __syncthreads();
-    for (uint32_t t = tid; t < MT * ng; t += GV_NT) {
-      uint32_t m = t / ng, g = t - m * ng;
-      const u32x4 *x4 = (const u32x4 *)(sX + m * KSM + g * UK);
-      float lo = 0.0f, hi = 0.0f;
+    if constexpr (WE != W_F16) {
+      const f16x2 a = as_h2(v.x), b = as_h2(v.y), c = as_h2(v.z), d = as_h2(v.w);
+      float lo = ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
+      float hi = ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
 #pragma unroll
-      for (int q = 0; q < UK / 8; q++) {
-        const u32x4 xv = x4[q];
-        const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
-        lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
-        hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
+      for (int o = 1; o < UK / 8; o *= 2) {
+        lo += __shfl_xor(lo, o);
+        hi += __shfl_xor(hi, o);
       }
-      sG[m * NGM + g] = (f32x2){lo, hi};
+      if (kq % (UK / 8) == 0) sG[m * NGM + kq / (UK / 8)] = (f32x2){lo, hi};
     }
   }
   __syncthreads();
@@ -282,13 +342,14 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 #pragma unroll
   for (int j = 0; j < PF; j++)
     if (j0 + j < nuw) compute(ring[j], u0 + j0 + j);
-  __syncthreads();                                             // X' is dead: the buffer takes the partials
+  if constexpr (!SEP) __syncthreads();                         // X' is dead: the buffer takes the partials
 
   // the K-quarters meet in LDS
 #pragma unroll
   for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + ch * 64 + lane] = acc[m];
   __syncthreads();
-  finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
+  if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
+  else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -517,7 +578,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 #pragma unroll
     for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + ch * 64 + 16 * i + l16] = acc[i][r];
   __syncthreads();
-  finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
+  if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
+  else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
 static uint32_t ks_max_of(uint32_t M, bool mf) {
