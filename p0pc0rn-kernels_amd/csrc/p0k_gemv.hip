@@ -371,7 +371,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 template <int WE>
 struct MUnit;
 template <>
-struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 8; u32x4 code; uint32_t sm; };   // row `lane`, as loaded
+struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 4; u32x4 code; uint32_t sm; };   // row `lane`, as loaded
 template <>
 struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x2 code[4][2]; uint32_t s[4]; };
 template <>
