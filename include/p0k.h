@@ -195,6 +195,15 @@ int p0k_sync(p0k_ctx *ctx);
 int p0k_gemm_check(const p0k_gemm_args *a);                    /* validation only (no context, no GPU) */
 int p0k_gemm(p0k_ctx *ctx, const p0k_gemm_args *a);            /* validate + enqueue; returns the status */
 double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the reference's return value (gemm.js:326) */
+/* p0k_gemm_noalloc: p0k_gemm that allocates nothing. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * same kernels, with every workspace (split-decode partials and counters, the rms / lnmod / PixelNorm X', the conv3
+ * zero block) taken from one static device array per GPU, set up when the first context on that GPU is created.
+ * A call needing more than p0k_gemm_noalloc_scratch_bytes() (31.5 MiB: e.g. X' of M * K * 2 bytes) is refused with
+ * P0K_E_ARG. All calls on one GPU share the array, so calls that overlap in time on one GPU (other streams, other
+ * contexts) race; calls in order on one stream do not. Results are the same bits as p0k_gemm's. */
+int p0k_gemm_noalloc(p0k_ctx *ctx, const p0k_gemm_args *a);
+uint64_t p0k_gemm_noalloc_scratch_bytes(void);
 int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use (for a
                                                                    256-CU device and the current environment) */
 int p0k_rowstats_check(const p0k_rowstats_args *a);

@@ -36,6 +36,8 @@ int hip_err(hipError_t e, const char *what) {
 
 struct PooledBuf { void *ptr; uint64_t seq; };
 
+int scratch_setup(int device, hipStream_t s);   // the allocation-free gemm's per-device array (below)
+
 }  // namespace
 
 struct p0k_ctx {
@@ -101,6 +103,10 @@ int p0k_ctx_create(int device, p0k_ctx **out) {
     (void)hipStreamDestroy(c->stream);
     delete c;
     return hip_err(e, "workspace counters");
+  }
+  if (int rs = scratch_setup(device, c->stream)) {
+    p0k_ctx_destroy(c);
+    return rs;
   }
   *out = c;
   return P0K_OK;
@@ -355,7 +361,80 @@ static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t need, const
   return P0K_OK;
 }
 
-int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------ scratch
+// The allocation-free gemm (p0k_gemm_noalloc) takes every workspace from this array instead of the context's grown
+// buffers. Layout: [0, 256 KiB) one arrival counter per 128-column tile of the split decode (zero between calls:
+// the last item of a tile resets its counter), [256 KiB, +256) the zero block the conv3 gather's padding taps read,
+// [512 KiB, 32 MiB) either the split decode's fp32 partials or the rms / lnmod / PixelNorm X' of one call. Each
+// device holds its own copy; host code reaches it only through the address hipGetSymbolAddress returns for that
+// device (the array's name on the host is a stand-in, not a device address).
+static constexpr uint64_t SCRATCH_BYTES = 32ull << 20, SCRATCH_CNT = 0, SCRATCH_ZERO = 256ull << 10,
+                          SCRATCH_WS = 512ull << 10;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[MAX_DEVICES];
+
+__global__ void k_zero_words(uint32_t *p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// once per device, with that device current and from a context's set-up (not under graph capture): resolve the
+// device address of `scratch` and clear its counters and zero block with a fill kernel
+int scratch_setup(int device, hipStream_t s) {
+  if (device < 0 || device >= MAX_DEVICES) return set_err(P0K_E_UNSUPPORTED, "scratch: device ordinal out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[device]) return P0K_OK;
+  void *ptr = nullptr;
+  HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  const uint32_t words = (uint32_t)((SCRATCH_ZERO + 256) / 4);
+  hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, s, (uint32_t *)ptr, words);
+  HIPCHK(hipGetLastError(), "scratch clear launch");
+  HIPCHK(hipStreamSynchronize(s), "hipStreamSynchronize");
+  g_scratch_ptr[device] = (uint8_t *)ptr;
+  return P0K_OK;
+}
+}  // namespace
+
+// Where one call's workspaces come from: the context's buffers, grown on demand (p0k_gemm), or the device's scratch
+// array, refused when too small (p0k_gemm_noalloc).
+struct WsSource {
+  p0k_ctx *c;
+  uint8_t *scratch;   // non-null: the allocation-free path
+  int part(uint64_t need, float **out) {
+    if (scratch) {
+      if (need > SCRATCH_BYTES - SCRATCH_WS)
+        return set_err(P0K_E_ARG, "gemm_noalloc: the split decode needs " + std::to_string(need) +
+                                      " bytes of partials, the scratch array holds " +
+                                      std::to_string(SCRATCH_BYTES - SCRATCH_WS));
+      *out = (float *)(scratch + SCRATCH_WS);
+      return P0K_OK;
+    }
+    if (int r = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "decode")) return r;
+    *out = c->ws_part;
+    return P0K_OK;
+  }
+  int xws(uint64_t need, void **out) {
+    if (scratch) {
+      if (need > SCRATCH_BYTES - SCRATCH_WS)
+        return set_err(P0K_E_ARG, "gemm_noalloc: the prologue needs " + std::to_string(need) +
+                                      " bytes of X', the scratch array holds " + std::to_string(SCRATCH_BYTES - SCRATCH_WS));
+      *out = scratch + SCRATCH_WS;
+      return P0K_OK;
+    }
+    if (int r = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return r;
+    *out = c->ws_x;
+    return P0K_OK;
+  }
+  uint32_t *counters() { return scratch ? (uint32_t *)(scratch + SCRATCH_CNT) : c->ws_cnt; }
+  const void *zero() { return scratch ? (const void *)(scratch + SCRATCH_ZERO) : c->ws_zero; }
+};
+
+static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
   if (!c) return set_err(P0K_E_ARG, "gemm: NULL context");
   std::string err;
   p0k::Params p;
@@ -386,31 +465,34 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   hipError_t e;
   if (plan.kernel == p0k::K_GEMV || plan.kernel == p0k::K_GEMV_MF) {
     const uint32_t tiles = (a->N + 127) / 128;
+    float *part = nullptr;
     if (plan.S > 1) {
       if (tiles > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "gemm: N too large for the decode workspace");
       const uint64_t need = (uint64_t)plan.S * a->M * tiles * 128u * sizeof(float);
-      if (int rr = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "decode")) return rr;
+      if (int rr = ws.part(need, &part)) return rr;
     }
-    e = p0k::launch_gemv(p, plan.we, plan.xm, c->ws_part, c->ws_cnt, plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF);
+    e = p0k::launch_gemv(p, plan.we, plan.xm, part, ws.counters(), plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF);
   } else if (plan.kernel == p0k::K_MFMA_DMA && plan.xm == P0K_X_CONV3) {
-    p.Z = (const uint8_t *)c->ws_zero;
+    p.Z = (const uint8_t *)ws.zero();
     if (p.flags & p0k::F_PN) {
       // PixelNorm + SiLU once per input element into the X' workspace; the gather then reads plain fp16 voxels
       const uint64_t need = (uint64_t)p.nvox * p.Ci * 2u;
-      if (int rr = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return rr;
-      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)c->ws_x, c->stream);
+      void *xw = nullptr;
+      if (int rr = ws.xws(need, &xw)) return rr;
+      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)xw, c->stream);
       if (e != hipSuccess) return hip_err(e, "gemm prologue launch");
-      p.X = (const uint8_t *)c->ws_x;
+      p.X = (const uint8_t *)xw;
     }
     e = p0k::launch_gemm_dma(p, plan.we, P0K_X_CONV3, plan.bm, plan.bn, tune.cus, false, c->stream);
   } else if (plan.kernel == p0k::K_MFMA_DMA) {
     if (plan.xm != P0K_X_F16) {
       // the prologue once per element into the X' workspace; the GEMM then reads fp16 rows
       const uint64_t need = (uint64_t)a->M * a->K * 2u;
-      if (int rr = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return rr;
-      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)c->ws_x, c->stream);
+      void *xw = nullptr;
+      if (int rr = ws.xws(need, &xw)) return rr;
+      e = p0k::launch_xprep(p, plan.xm, (uint16_t *)xw, c->stream);
       if (e != hipSuccess) return hip_err(e, "gemm prologue launch");
-      p.X = (const uint8_t *)c->ws_x;
+      p.X = (const uint8_t *)xw;
       p.ldx = a->K;
       p.kx0 = 0;
     }
@@ -421,6 +503,23 @@ int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) {
   if (e != hipSuccess) return hip_err(e, "gemm launch");
   return P0K_OK;
 }
+
+extern "C" {
+
+int p0k_gemm(p0k_ctx *c, const p0k_gemm_args *a) { return gemm_run(c, a, WsSource{c, nullptr}); }
+
+int p0k_gemm_noalloc(p0k_ctx *c, const p0k_gemm_args *a) {
+  if (!c) return set_err(P0K_E_ARG, "gemm_noalloc: NULL context");
+  uint8_t *sp;
+  {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    sp = (c->device >= 0 && c->device < MAX_DEVICES) ? g_scratch_ptr[c->device] : nullptr;
+  }
+  if (!sp) return set_err(P0K_E_UNSUPPORTED, "gemm_noalloc: the scratch array of this device is not set up");
+  return gemm_run(c, a, WsSource{c, sp});
+}
+
+uint64_t p0k_gemm_noalloc_scratch_bytes(void) { return SCRATCH_BYTES - SCRATCH_WS; }
 
 int p0k_rowstats_check(const p0k_rowstats_args *a) {
   std::string err;
