@@ -152,7 +152,7 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) sacc[kb][r] = p.cap * tanhf(sacc[kb][r] * p.scale / p.cap);
+        for (int r = 0; r < 16; r++) sacc[kb][r] = p.cap * (2.0f * sigmoid(2.0f * sacc[kb][r] * p.scale / p.cap) - 1.0f);
       sf = 1.4426950408889634f;
     }
     const uint32_t kl = qlim > k0 ? qlim - k0 : 0u;           // keys of this tile the lane's query sees: [0, kl)

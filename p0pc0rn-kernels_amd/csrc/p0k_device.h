@@ -128,7 +128,12 @@ __device__ __forceinline__ u32x4 xperm(u32x4 v) {
 }
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return as_u((f16x2){(f16)a, (f16)b}); }
-__device__ __forceinline__ float silu(float z) { return z / (1.0f + __expf(-z)); }
+// e^x as 2^(x log2 e) on the hardware exp2 (v_exp_f32) and 1 / x on the hardware reciprocal (v_rcp_f32), each
+// within about one fp32 ulp, far inside the fp16 rounding of every result they feed; the logistic function
+// 1 / (1 + e^-x) from them saturates cleanly (e^-x = inf -> 0)
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float silu(float z) { return z * sigmoid(z); }
 
 // ----------------------------------------------------------------------------------------------- prologue
 // Row context of the implicit-GEMM convolutions: computed once per row, reused for every k step.
@@ -226,14 +231,15 @@ __device__ __forceinline__ void store_f16x8(uint8_t *yb, size_t idx, const float
   }
 }
 
-// the GLU activation of gemm.js:205-209: SiLU g / (1 + e^-g), or tanh-GELU with its argument clamped to +-15
+// the GLU activation of gemm.js:205-209: SiLU g / (1 + e^-g), or tanh-GELU g (1 + tanh z) / 2 with its argument z
+// clamped to +-15, computed as g * sigmoid(2 z) (the same function: (1 + tanh z) / 2 = 1 / (1 + e^-2z))
 __device__ __forceinline__ float glu_act(float gt, bool gelu) {
   if (gelu) {
     float z = 0.7978845608f * (gt + 0.044715f * gt * gt * gt);
     z = fminf(fmaxf(z, -15.0f), 15.0f);
-    return gt * 0.5f * (1.0f + tanhf(z));
+    return gt * sigmoid(2.0f * z);
   }
-  return gt / (1.0f + __expf(-gt));
+  return silu(gt);
 }
 
 // sum over the 16 lanes of an aligned lane group (the 16 threads that share one row in the epilogue)
@@ -330,7 +336,7 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
       if (live && col < p.N) {
         const uint16_t *gt = p.GT + (size_t)m * p.Ltot + p.ny0 + col;
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = v[j] * inv * p.EV[p.evOff + g * 8 + j] / (1.0f + __expf(-h_val(gt[j])));
+        for (int j = 0; j < 8; j++) v[j] = v[j] * inv * p.EV[p.evOff + g * 8 + j] * sigmoid(h_val(gt[j]));
         store_f16x8(p.Y, (size_t)m * p.ldy + p.ny0 + col, v, p.N - col);
       }
       continue;
