@@ -47,7 +47,7 @@ MALL = 256 << 20
 # FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run, so the
 # figures of the last profiled build are kept here, per workload.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36133, 28), "decode_q4_swiglu_M16": (36900, 448)}
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35993, 28), "decode_q4_swiglu_M16": (36567, 448)}
 
 
 def log(msg):
@@ -282,25 +282,43 @@ def time_workload(dev, wl, steps, warmup):
         dev.event_destroy(e0)
         dev.event_destroy(e1)
         return ms, ms, steps, None
+    # exactly `steps` timed calls: `reps` replays of a graph of `per_graph` calls (a multiple of the rotation), then
+    # one replay of a graph with the remaining calls; the per-call distribution comes from the full replays
     per_graph = max(len(structs), min(steps, 64 if wl.bound == "hbm" else 8))
     per_graph -= per_graph % len(structs)
-    dev.graph_begin()
-    try:
-        for i in range(per_graph):
-            run(structs[i % len(structs)])
-    finally:
-        g = dev.graph_end()
-    reps = max(1, -(-steps // per_graph))
-    for _ in range(max(1, -(-warmup // per_graph))):
+    reps, rem = divmod(steps, per_graph)
+    if reps == 0:
+        reps, rem, per_graph = 1, 0, steps
+
+    def capture(n, first):
+        dev.graph_begin()
+        try:
+            for i in range(n):
+                run(structs[(first + i) % len(structs)])
+        finally:
+            g = dev.graph_end()
+        return g
+    g = capture(per_graph, 0)
+    gr = capture(rem, reps * per_graph) if rem else None
+    wreps, wrem = divmod(warmup, per_graph)                 # exactly `warmup` untimed calls
+    for _ in range(wreps):
         dev.graph_launch(g)
+    if wrem:
+        gw = capture(wrem, 0)
+        dev.graph_launch(gw)
+        dev.done()
+        dev.graph_destroy(gw)
     dev.done()
     # one event before each replay and one after the last: the whole timed region, and per replay the time per call
-    ev = [dev.event() for _ in range(reps + 1)]
+    ev = [dev.event() for _ in range(reps + 2)]
     t0 = time.perf_counter()
     dev.record(ev[0])
     for i in range(reps):
         dev.graph_launch(g)
         dev.record(ev[i + 1])
+    if gr is not None:
+        dev.graph_launch(gr)
+    dev.record(ev[-1])
     dev.done()
     wall = time.perf_counter() - t0
     ms = dev.elapsed_ms(ev[0], ev[-1])
@@ -308,10 +326,13 @@ def time_workload(dev, wl, steps, warmup):
     for e in ev:
         dev.event_destroy(e)
     dev.graph_destroy(g)
-    n = reps * per_graph
+    if gr is not None:
+        dev.graph_destroy(gr)
+    n = reps * per_graph + rem
+    assert n == steps
     q = lambda f: per[min(reps - 1, int(f * reps))]   # noqa: E731
     dist = {"p10": round(q(0.1), 5), "median": round(q(0.5), 5), "p90": round(q(0.9), 5), "replays": reps,
-            "calls_per_replay": per_graph}
+            "calls_per_replay": per_graph, "remainder_calls": rem}
     return ms / n, wall / n * 1e3, n, dist
 
 
@@ -349,8 +370,8 @@ def cpu_baseline(config, rows, target_s=0.0):
 
 CPU_HEADLINE_S = 10.0   # seconds of CPU work timed for the headline workload (whole calls, repeated)
 CPU_SAMPLE = {   # workload -> (cpu_ref config, rows of M timed)
-    "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 1), "decode_q4_swiglu_M16": ("decode", 1),
-    "prefill_q8_rms_resadd": ("prefill", 1), "dit_qkv_q4_lnmod_heads": ("dit_qkv", 1), "dit_up_q4_geglu": ("dit_up", 1),
+    "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 4), "decode_q4_swiglu_M16": ("decode", 8),
+    "prefill_q8_rms_resadd": ("prefill", 8), "dit_qkv_q4_lnmod_heads": ("dit_qkv", 8), "dit_up_q4_geglu": ("dit_up", 8),
     "conv3_128_T13x92x160": ("conv3", 64),
 }
 
