@@ -283,7 +283,7 @@ function groupnormStats(gpu, a) { call(addon().gn, gpu.ctx, gnDesc(a), 3); }
 /** per-device tile / accumulation choices; matched against gpu.info like the reference's table */
 const TUNE_TABLE = [
   { match: { vendor: 'amd', architecture: 'gfx950' }, tune: {},
-    source: 'MI355X: libp0k picks its own MFMA tiles (128x128) and the streaming GEMV for M <= 16; the tile only matters for range checks' },
+    source: 'MI355X: libp0k picks its own CDNA4 kernel and tile per call (streaming GEMV for M <= 16, load-to-LDS MFMA GEMM with 128/256 x 128/256 tiles above); the tile only matters for range checks' },
 ];
 
 function tuneEntry(g, table = TUNE_TABLE) {
@@ -299,9 +299,10 @@ function defaultTune(g, o = {}) {
   return g.tune;
 }
 
-/** measure GEMM throughput (q4, M=1024 N=3072 K=3072, both accumulation modes); sets gpu.rate and gpu.calib */
+/** measure GEMM throughput (q4, M=1024 N=3072 K=3072, both accumulation modes) and attention throughput (8 heads of
+ *  128, 1024 x 1024); sets gpu.rate (mm32, mm16, mm, attn) and gpu.calib, as src/core/tune.js:39-58 does */
 async function calibrate(g) {
-  const M = 1024, N = 3072, K = 3072;
+  const M = 1024, N = 3072, K = 3072, L = 1024, H = 8;
   const recs = (N / 64) * (K / 32), u = new Uint32Array(recs * 320);
   let s = 0x9e3779b9 | 0;
   const next = () => { s = (Math.imul(s, 1664525) + 1013904223) | 0; return s >>> 0; };
@@ -309,9 +310,9 @@ async function calibrate(g) {
     for (let j = 0; j < 256; j++) u[r * 320 + j] = next();
     for (let j = 0; j < 64; j++) u[r * 320 + 256 + j] = 0x2000 | ((0xa800 | (j & 0x3f)) << 16);   // scale 2^-11, min -2^-6-ish
   }
-  const xs = new Uint16Array(M * K);
-  for (let i = 0; i < xs.length; i++) xs[i] = (next() & 0x83ff) | 0x3400;
-  const W = g.upload(u), X = g.upload(xs), Y = g.buffer(M * N * 2);
+  const h16 = (n) => { const h = new Uint16Array(n); for (let i = 0; i < n; i++) h[i] = (next() & 0x83ff) | 0x3400; return h; };
+  const W = g.upload(u), X = g.upload(h16(M * K)), Y = g.buffer(M * N * 2);
+  const Q = g.upload(h16(H * L * 128)), O = g.buffer(L * H * 256);
   const time = async (fn, reps) => { fn(); await g.done(); const t0 = process.hrtime.bigint(); for (let i = 0; i < reps; i++) fn(); await g.done(); return Number(process.hrtime.bigint() - t0) / 1e9 / reps; };
   try {
     const mm = (acc) => time(() => gemm(g, { w: { buf: W, off: 0, bytes: W._pf, enc: 'q4g32a.t64', rows: N, cols: K }, x: { buf: X }, M, N, K, epi: 'f16', y: { buf: Y }, acc }), 20);
@@ -319,9 +320,12 @@ async function calibrate(g) {
     g.rate.mm32 = 0.8 * (2 * M * N * K) / t32;
     g.rate.mm16 = 0.8 * (2 * M * N * K) / t16;
     g.rate.mm = Math.min(g.rate.mm32, g.rate.mm16);
-    g.calib = { gemmF32Gflops: Math.round(2 * M * N * K / t32 / 1e9), gemmF16Gflops: Math.round(2 * M * N * K / t16 / 1e9) };
+    const ta = await time(() => attention(g, { q: { buf: Q }, k: { buf: Q }, v: { buf: Q }, o: { buf: O }, Lq: L, Lk: L, Hq: H, Hkv: H, mode: 0 }), 20);
+    g.rate.attn = 0.8 * (4 * L * L * 128 * H) / ta;
+    g.calib = { gemmF32Gflops: Math.round(2 * M * N * K / t32 / 1e9), gemmF16Gflops: Math.round(2 * M * N * K / t16 / 1e9),
+      attnGflops: Math.round(4 * L * L * 128 * H / ta / 1e9) };
   } finally {
-    [W, X, Y].forEach((b) => g.free(b));
+    [W, X, Y, Q, O].forEach((b) => g.free(b));
   }
   return g.calib;
 }
@@ -433,10 +437,113 @@ function encodedBytes(enc, rows, cols) {
   return addon().tensorBytes(ENC[enc], rows, cols);
 }
 
+// ------------------------------------------------------------------ converter helpers (src/convert/encode.js)
+// What loadWeights callers use to produce the manifest tensors: raw safetensors bytes -> fp32, the matrix view of a
+// tensor (convolution weights reordered so each output channel's row is the implicit GEMM's K vector, the OHWI /
+// OTHWI layouts the conv / conv3 prologues read), the encoding rule, and the row encoders.
+const DTYPE_BYTES = { F32: 4, F16: 2, BF16: 2, F8_E4M3: 1, F8_E5M2: 1 };
+function dtypeBytes(dt) {
+  if (!DTYPE_BYTES[dt]) throw new Error('unsupported dtype ' + dt + ' (F32, F16, BF16, F8_E4M3, F8_E5M2)');
+  return DTYPE_BYTES[dt];
+}
+/** the 256 values of an 8-bit float: e4m3 (bias 7, no infinities, 0x7f / 0xff NaN) or e5m2 (bias 15, IEEE-style) */
+function fp8Values(e4m3) {
+  const mb = e4m3 ? 3 : 2, bias = e4m3 ? 7 : 15, out = new Float32Array(256);
+  for (let b = 0; b < 256; b++) {
+    const sign = b & 0x80 ? -1 : 1, e = (b & 0x7f) >> mb, m = b & ((1 << mb) - 1), emax = e4m3 ? 15 : 31;
+    if (e4m3 && e === emax && m === (1 << mb) - 1) out[b] = NaN;
+    else if (!e4m3 && e === emax) out[b] = m ? NaN : sign * Infinity;
+    else if (e === 0) out[b] = sign * m * 2 ** (1 - bias - mb);
+    else out[b] = sign * ((1 << mb) + m) * 2 ** (e - bias - mb);
+  }
+  return out;
+}
+const FP8 = {};
+/** raw tensor bytes of a safetensors dtype -> Float32Array */
+function toFloat32(dtype, bytes) {
+  const u8 = bytes instanceof Uint8Array ? bytes : new Uint8Array(bytes), n = u8.byteLength / dtypeBytes(dtype);
+  const out = new Float32Array(n);
+  if (dtype === 'F32') { new Uint8Array(out.buffer).set(u8); return out; }
+  if (dtype === 'F8_E4M3' || dtype === 'F8_E5M2') {
+    const t = FP8[dtype] || (FP8[dtype] = fp8Values(dtype === 'F8_E4M3'));
+    for (let i = 0; i < n; i++) out[i] = t[u8[i]];
+    return out;
+  }
+  const h = new Uint16Array(n);
+  new Uint8Array(h.buffer).set(u8);
+  if (dtype === 'BF16') { const w = new Uint32Array(out.buffer); for (let i = 0; i < n; i++) w[i] = h[i] << 16; return out; }
+  for (let i = 0; i < n; i++) out[i] = h2f(h[i]);
+  return out;
+}
+/** {header, dataStart} of a safetensors file from its first bytes (8-byte length + JSON header) */
+function safetensorsHeader(bytes) {
+  const u8 = bytes instanceof Uint8Array ? bytes : new Uint8Array(bytes);
+  const n = Number(new DataView(u8.buffer, u8.byteOffset, u8.byteLength).getBigUint64(0, true));
+  if (n > 100e6 || 8 + n > u8.byteLength) throw new Error('safetensors: bad or truncated header');
+  return { header: JSON.parse(Buffer.from(u8.subarray(8, 8 + n)).toString('utf8')), dataStart: 8 + n };
+}
+/** the tensors of a header in file order: [{name, dtype, shape, begin, end}] (offsets from the data start) */
+function safetensorsList(header) {
+  const out = [];
+  for (const [name, t] of Object.entries(header)) {
+    if (name === '__metadata__') continue;
+    out.push({ name, dtype: t.dtype, shape: t.shape, begin: t.data_offsets[0], end: t.data_offsets[1] });
+  }
+  return out.sort((a, b) => a.begin - b.begin);
+}
+/** the matrix a tensor is stored as: 2-D as is; [O, I, kh, kw] -> OHWI rows; [O, I, kt, kh, kw] -> OTHWI rows; vectors;
+ *  other ranks flatten their leading dimensions */
+function matrixOf(shape) {
+  const prod = (a) => a.reduce((x, y) => x * y, 1);
+  if (shape.length === 4) return { rows: shape[0], cols: prod(shape.slice(1)), layout: 'OHWI' };
+  if (shape.length === 5) return { rows: shape[0], cols: prod(shape.slice(1)), layout: 'OTHWI' };
+  if (shape.length <= 1) return { rows: 1, cols: shape.length ? shape[0] : 1, layout: 'vector' };
+  return { rows: prod(shape.slice(0, -1)), cols: shape[shape.length - 1], layout: 'row-major' };
+}
+/** convolution weight rows from the framework's OIHW / OITHW order (input channel outer, tap inner) to the kernels'
+ *  OHWI / OTHWI order (tap outer, input channel inner); returns a new Float32Array */
+function reorderConvRows(W, rows, shape) {
+  const I = shape[1], taps = shape.slice(2).reduce((x, y) => x * y, 1), K = I * taps, out = new Float32Array(rows * K);
+  for (let r = 0; r < rows; r++) {
+    const o = r * K;
+    for (let i = 0; i < I; i++) for (let t = 0; t < taps; t++) out[o + t * I + i] = W[o + i * taps + t];
+  }
+  return out;
+}
+/** the encoding a tensor gets: f32 for vectors (and names matching opts.f32), f16 for names matching opts.keep or
+ *  bits 16, q4 / q8 for matrices whose rows and columns fit the record tiles (bits 4 or 8), f16 otherwise */
+function chooseEncoding(name, shape, opts = {}) {
+  const bits = opts.bits || 4, m = matrixOf(shape);
+  if (opts.f32 && opts.f32.test(name)) return 'f32';
+  if (m.layout === 'vector') return 'f32';
+  if ((opts.keep && opts.keep.test(name)) || bits === 16) return 'f16';
+  if (bits === 4 && m.rows % 64 === 0 && m.cols % 32 === 0) return 'q4g32a.t64';
+  if ((bits === 4 || bits === 8) && m.rows % 64 === 0 && m.cols % 64 === 0) return 'q8g64s.t64';
+  return 'f16';
+}
+/** fp32 bytes of W */
+function packF32(W) { return new Uint8Array(Float32Array.from(W).buffer); }
+/** bytes of one 64-row tile of K columns in an encoding */
+function tileBytes(enc, K) {
+  if (enc === 'q4g32a.t64') return (K / 32) * 1280;
+  if (enc === 'q8g64s.t64') return (K / 64) * 4224;
+  return 64 * K * (enc === 'f16' ? 2 : 4);
+}
+/** rows x K fp32 values in an encoding (rows a multiple of 64 for q4 / q8) -> Uint8Array */
+function encodeRows(enc, W, rows, K) {
+  const w = asF32(W);
+  if (enc === 'q4g32a.t64') return packQ4(w, rows, K);
+  if (enc === 'q8g64s.t64') return packQ8(w, rows, K);
+  if (enc === 'f16') return packF16(w.subarray(0, rows * K));
+  if (enc === 'f32') return packF32(w.subarray(0, rows * K));
+  throw new Error('unknown encoding ' + enc);
+}
+
 export {
   MB, GpuError, createGpu, Gpu, f2h, h2f, toF16, fromF16,
   gemm, gemmPlan, gemmDesc, DEFAULT_TILE, rowstats, attention, pixstats, gnPartBytes, gnPartial, gnFinalize, groupnormStats,
   TUNE_TABLE, tuneEntry, defaultTune, calibrate,
   MANIFEST_FORMAT, loadWeights, uploadWeights,
-  packQ4, packQ8, packF16, encodedBytes,
+  packQ4, packQ8, packF16, packF32, encodedBytes, tileBytes, encodeRows,
+  dtypeBytes, toFloat32, safetensorsHeader, safetensorsList, matrixOf, reorderConvRows, chooseEncoding,
 };

@@ -5,6 +5,9 @@
 //                             createGpu → upload → gemm → read → <out>_gpu.bin
 //   run_case.mjs weights <dir> GPU: loadWeights on a converted-model folder, then gemm with model.tensor(...)
 //   run_case.mjs stats <dir>  GPU: pixstats and groupnormStats
+//   run_case.mjs convert <dir> no GPU: the converter helpers (toFloat32, safetensors header, matrixOf, chooseEncoding,
+//                             reorderConvRows, encodeRows, tileBytes) on inputs written by the test
+//   run_case.mjs calibrate <dir> GPU: calibrate() -> gpu.rate / gpu.calib
 'use strict';
 import { readFileSync, writeFileSync } from 'fs';
 import { join } from 'path';
@@ -110,5 +113,40 @@ async function stats() {
   await g.done(); g.destroy();
 }
 
-const run = { host, gemm: gemmCase, weights, stats }[mode];
+async function convert() {
+  const spec = JSON.parse(readFileSync(join(dir, 'spec.json'), 'utf8'));
+  const res = {};
+  for (const [dt, file] of Object.entries(spec.raw)) put('f32_' + dt + '.f32', p0k.toFloat32(dt, bin(file)));
+  const st = bin('model.safetensors');
+  const { header, dataStart } = p0k.safetensorsHeader(st);
+  res.list = p0k.safetensorsList(header);
+  res.dataStart = dataStart;
+  const conv = res.list.find((t) => t.name === spec.conv);
+  const Wc = p0k.toFloat32(conv.dtype, st.subarray(dataStart + conv.begin, dataStart + conv.end));
+  const m = p0k.matrixOf(conv.shape);
+  res.matrix = m;
+  res.enc = p0k.chooseEncoding(conv.name, conv.shape, { bits: 16 });
+  const Wr = p0k.reorderConvRows(Wc, m.rows, conv.shape);
+  put('conv_reordered.f32', Wr);
+  put('conv_f16.bin', p0k.encodeRows(res.enc, Wr, m.rows, m.cols));
+  res.matrices = spec.shapes.map((sh) => p0k.matrixOf(sh));
+  res.encodings = spec.choose.map(([n, sh, o]) => p0k.chooseEncoding(n, sh, o ? { bits: o.bits, keep: o.keep && new RegExp(o.keep), f32: o.f32 && new RegExp(o.f32) } : {}));
+  res.tileBytes = ['q4g32a.t64', 'q8g64s.t64', 'f16', 'f32'].map((e) => p0k.tileBytes(e, 256));
+  const W = new Float32Array(bin('W.f32').slice().buffer);
+  put('enc_q4.bin', p0k.encodeRows('q4g32a.t64', W, 64, 256));
+  put('enc_q8.bin', p0k.encodeRows('q8g64s.t64', W, 64, 256));
+  put('enc_f32.bin', p0k.encodeRows('f32', W, 64, 256));
+  res.badDtype = errorOf(() => p0k.toFloat32('I64', new Uint8Array(8)));
+  res.badEnc = errorOf(() => p0k.encodeRows('q5', W, 64, 256));
+  writeFileSync(join(dir, 'result.json'), JSON.stringify(res));
+}
+
+async function calibrate() {
+  const g = await p0k.createGpu();
+  const calib = await p0k.calibrate(g);
+  writeFileSync(join(dir, 'result.json'), JSON.stringify({ calib, rate: g.rate }));
+  await g.done(); g.destroy();
+}
+
+const run = { host, gemm: gemmCase, weights, stats, convert, calibrate }[mode];
 run().catch((e) => { console.error(e && e.stack || e); process.exit(1); });

@@ -181,3 +181,115 @@ def test_shim_pixstats_groupnorm_attention(tmp_path):
     ab = np.fromfile(str(tmp_path / "ab_gpu.f32"), np.float32)[:2 * GC]
     want = oracle.gn_finalize(oracle.gn_partial(gx, pix, GC), (pix + 63) // 64, GC, g, b, 1e-6)
     np.testing.assert_allclose(ab, want, rtol=2e-6, atol=1e-7)
+
+
+def _safetensors(tensors):
+    """a safetensors file: 8-byte header length, JSON header (dtype, shape, data_offsets), then the data"""
+    header, blobs, off = {"__metadata__": {"format": "pt"}}, [], 0
+    for name, (dtype, shape, raw) in tensors.items():
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    return len(h).to_bytes(8, "little") + h + b"".join(blobs)
+
+
+def test_converter_helpers(tmp_path):
+    """The converter helpers of src/convert/encode.js:40-133 that loadWeights callers use, with known answers: fp8 / bf16
+    / fp16 decoding (e4m3 0x38 = 1, 0x7e = 448, 0x01 = 2^-9, 0x7f NaN; e5m2 0x3c = 1, 0x7b = 57344, 0x7c = inf,
+    0x01 = 2^-16; bf16 0x3f80 = 1), the matrix view and encoding rule of each tensor rank, the OITHW -> OTHWI row order
+    against numpy's transpose, and encodeRows against the oracle's encoders."""
+    rng = np.random.default_rng(12)
+    e4 = np.arange(256, dtype=np.uint8)
+    raw = {"F8_E4M3": e4, "F8_E5M2": e4, "BF16": np.array([0x3F80, 0xC000, 0x0000, 0x7F80, 0x3E80], np.uint16),
+           "F16": oracle.f16_bits(np.array([1.0, -2.0, 65504.0, 2 ** -24], np.float32)),
+           "F32": np.array([1.5, -0.25, 3e38], np.float32)}
+    for dt, a in raw.items():
+        a.tofile(str(tmp_path / f"raw_{dt}.bin"))
+    N, C = 64, 32
+    Wc = oracle.h2f(oracle.f16_bits((rng.standard_normal(N * C * 27) * 0.05).astype(np.float32)))
+    st = _safetensors({"vae.conv3.weight": ("F32", (N, C, 3, 3, 3), Wc.astype(np.float32).tobytes()),
+                       "vae.norm.bias": ("F16", (N,), oracle.f16_bits(np.ones(N, np.float32)).tobytes())})
+    (tmp_path / "model.safetensors").write_bytes(st)
+    W = (rng.standard_normal(64 * 256) * 0.05).astype(np.float32)
+    W.tofile(str(tmp_path / "W.f32"))
+    shapes = [[128, 64, 3, 3], [128, 64, 3, 3, 3], [96], [], [4, 8, 256], [3072, 3072]]
+    choose = [["a", [3072, 3072], None], ["a", [3072, 3072], {"bits": 8}], ["a", [3072, 3072], {"bits": 16}],
+              ["a.norm", [3072], None], ["a.keep", [3072, 3072], {"keep": "keep"}], ["a.f32", [64, 64], {"f32": "f32$"}],
+              ["a", [100, 3072], None], ["a", [128, 96], None], ["a", [128, 96], {"bits": 8}]]
+    (tmp_path / "spec.json").write_text(json.dumps({"raw": {dt: f"raw_{dt}.bin" for dt in raw}, "conv": "vae.conv3.weight",
+                                                    "shapes": shapes, "choose": choose}))
+    node("convert", tmp_path)
+    res = json.loads((tmp_path / "result.json").read_text())
+
+    f8 = np.fromfile(str(tmp_path / "f32_F8_E4M3.f32"), np.float32)
+    assert (f8[0x38], f8[0x7E], f8[0x01], f8[0x08], f8[0xB8]) == (1.0, 448.0, 2.0 ** -9, 2.0 ** -6, -1.0)
+    assert np.isnan(f8[0x7F]) and np.isnan(f8[0xFF]) and np.isfinite(f8[0x7E])
+    f5 = np.fromfile(str(tmp_path / "f32_F8_E5M2.f32"), np.float32)
+    assert (f5[0x3C], f5[0x7B], f5[0x01], f5[0xBC]) == (1.0, 57344.0, 2.0 ** -16, -1.0)
+    assert f5[0x7C] == np.inf and f5[0xFC] == -np.inf and np.isnan(f5[0x7D])
+    # every finite e5m2 value is the fp16 with the same top byte (e5m2 is truncated binary16)
+    fin = np.isfinite(f5)
+    np.testing.assert_array_equal(f5[fin], oracle.h2f((e4[fin].astype(np.uint16) << 8)))
+    assert list(np.fromfile(str(tmp_path / "f32_BF16.f32"), np.float32)) == [1.0, -2.0, 0.0, np.inf, 0.25]
+    assert list(np.fromfile(str(tmp_path / "f32_F16.f32"), np.float32)) == [1.0, -2.0, 65504.0, 2 ** -24]
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "f32_F32.f32"), np.float32), raw["F32"])
+
+    assert [t["name"] for t in res["list"]] == ["vae.conv3.weight", "vae.norm.bias"]
+    assert res["list"][0]["shape"] == [N, C, 3, 3, 3] and res["dataStart"] % 8 == 0
+    assert res["matrix"] == {"rows": N, "cols": C * 27, "layout": "OTHWI"} and res["enc"] == "f16"
+    want = Wc.reshape(N, C, 27).transpose(0, 2, 1).reshape(-1)                 # OITHW -> OTHWI
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "conv_reordered.f32"), np.float32), want)
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "conv_f16.bin"), np.uint16), oracle.f16_bits(want))
+    assert res["matrices"] == [{"rows": 128, "cols": 576, "layout": "OHWI"}, {"rows": 128, "cols": 1728, "layout": "OTHWI"},
+                               {"rows": 1, "cols": 96, "layout": "vector"}, {"rows": 1, "cols": 1, "layout": "vector"},
+                               {"rows": 32, "cols": 256, "layout": "row-major"},
+                               {"rows": 3072, "cols": 3072, "layout": "row-major"}]
+    assert res["encodings"] == ["q4g32a.t64", "q8g64s.t64", "f16", "f32", "f16", "f32", "f16", "q4g32a.t64", "f16"]
+    assert res["tileBytes"] == [8 * 1280, 4 * 4224, 64 * 256 * 2, 64 * 256 * 4]
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "enc_q4.bin"), np.uint8), oracle.pack_q4(W, 64, 256))
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "enc_q8.bin"), np.uint8), oracle.pack_q8(W, 64, 256))
+    np.testing.assert_array_equal(np.fromfile(str(tmp_path / "enc_f32.bin"), np.float32), W)
+    assert "unsupported dtype I64" in res["badDtype"]["message"] and "unknown encoding q5" in res["badEnc"]["message"]
+
+
+@pytest.mark.gpu
+def test_reordered_conv3_weights_run_conv3(dev, tmp_path):
+    """OITHW conv3 weights as a framework stores them -> the shim's reorderConvRows + encodeRows -> the conv3 GEMM on
+    the GPU, against a textbook 3-D cross-correlation with the OITHW weights (replicate-padded time, zero-padded
+    space)."""
+    rng = np.random.default_rng(13)
+    T, H, W, C, N = 4, 6, 10, 64, 128
+    Wc = oracle.h2f(oracle.f16_bits((rng.standard_normal(N * C * 27) * 0.03).astype(np.float32)))
+    (tmp_path / "model.safetensors").write_bytes(_safetensors({"c3": ("F32", (N, C, 3, 3, 3), Wc.tobytes())}))
+    np.zeros(64 * 256, np.float32).tofile(str(tmp_path / "W.f32"))
+    (tmp_path / "spec.json").write_text(json.dumps({"raw": {}, "conv": "c3", "shapes": [], "choose": []}))
+    node("convert", tmp_path)
+    wb = np.fromfile(str(tmp_path / "conv_f16.bin"), np.uint8)
+    c = make_conv3_case(T, H, W, C, N, seed=14)
+    c.bufs["w"] = wb
+    c.spec["w"]["bytes"] = wb.nbytes
+    got = oracle.h2f(c.run_device(dev)).astype(np.float64).reshape(T, H, W, N)
+    X = c.X.reshape(T, H, W, C).astype(np.float64)
+    Xp = np.pad(np.pad(X, ((1, 1), (0, 0), (0, 0), (0, 0)), mode="edge"), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    Wo = Wc.reshape(N, C, 3, 3, 3).astype(np.float64)
+    ref = np.zeros((T, H, W, N))
+    for kt in range(3):
+        for ky in range(3):
+            for kx in range(3):
+                ref += np.einsum("thwc,nc->thwn", Xp[kt:kt + T, ky:ky + H, kx:kx + W], Wo[:, :, kt, ky, kx])
+    err = np.abs(got - ref)
+    assert np.all(err <= 2 ** -9 * np.abs(ref) + 2 ** -10 * np.sqrt(np.mean(ref ** 2))), f"max err {err.max()}"
+
+
+@pytest.mark.gpu
+def test_calibrate_measures_gemm_and_attention(tmp_path):
+    """calibrate() (src/core/tune.js:39-58) sets gpu.rate.mm from timed q4 GEMMs and gpu.rate.attn from a timed
+    attention call."""
+    node("calibrate", tmp_path)
+    res = json.loads((tmp_path / "result.json").read_text())
+    for k in ("gemmF32Gflops", "gemmF16Gflops", "attnGflops"):
+        assert res["calib"][k] > 10000, res
+    assert res["rate"]["attn"] == pytest.approx(0.8 * res["calib"]["attnGflops"] * 1e9, rel=0.01)
+    assert res["rate"]["mm"] > 1e13
