@@ -277,36 +277,57 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
     }
     return;
   }
-  for (int r0 = 0; r0 < R; r0 += RPP) {
-    const int r = r0 + (tid >> 4);
-    const uint32_t m = mB + r;
-    const bool live = r < R && m < p.M;            // whole 16-lane groups agree, so the shuffles below are safe
-    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < R) {
-      const f32x4 *src = (const f32x4 *)(C + r * ldc + g * 8);
-      f32x4 a0 = src[0], a1 = src[1];
-      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+  if (epi == E_HEADS) {                                                            // gemm.js:216-253
+    // Q / K heads: RMSNorm over the head's 128 columns, the section's norm weights (loaded once here), RoPE from the
+    // table row of each output row (prefetched one pass ahead, so only the first pass waits for its loads); V raw
+    const uint32_t hd = nB >> 7;
+    const int sec = hd < p.Hq ? 0 : (hd < p.Hq + p.Hkv ? 1 : 2);
+    const int d0 = g * 8;
+    const bool half = p.flags & F_ROPE_HALF;
+    float nw[8];
+    if (sec < 2) {
+      const float *np = p.EV + p.evOff + (sec ? 128 : 0) + d0;   // ev.off is any float offset: scalar loads
+#pragma unroll
+      for (int j = 0; j < 8; j++) nw[j] = np[j];
     }
-    if (epi == E_HEADS) {                                                          // gemm.js:216-253
-      const uint32_t hd = nB >> 7;
-      const int sec = hd < p.Hq ? 0 : (hd < p.Hq + p.Hkv ? 1 : 2);
-      const int d0 = g * 8;
+    // the (cos, sin) values a thread reads for one row: interleaved, pairs d0 / 2 .. + 3 (8 floats at d0);
+    // rotate-half, angles (d0 + j) & 63, j = 0..7 (16 floats at 2 ((d0 & 63))); the table starts its buffer and a row
+    // is 512 bytes, so these are 16-byte aligned
+    auto rope_load = [&](int r0, f32x4 *dst) __attribute__((always_inline)) {
+      const int r = r0 + (tid >> 4);
+      const uint32_t m = mB + r, row = p.rowOff + (r < R && m < p.M ? m : 0u);
+      const f32x4 *rp4 = (const f32x4 *)(p.RP + (size_t)row * 128 + (half ? 2 * (d0 & 63) : d0));
+      dst[0] = rp4[0]; dst[1] = rp4[1];
+      if (half) { dst[2] = rp4[2]; dst[3] = rp4[3]; }
+    };
+    f32x4 rc[4], rn[4];
+    if (sec < 2) rope_load(0, rc);
+    for (int r0 = 0; r0 < R; r0 += RPP) {
+      const int r = r0 + (tid >> 4);
+      const uint32_t m = mB + r;
+      const bool live = r < R && m < p.M;          // whole 16-lane groups agree, so the shuffles below are safe
+      if (sec < 2 && r0 + RPP < R) rope_load(r0 + RPP, rn);
+      float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (r < R) {
+        const f32x4 *src = (const f32x4 *)(C + r * ldc + g * 8);
+        f32x4 a0 = src[0], a1 = src[1];
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+      }
       if (sec < 2) {
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) ss += v[j] * v[j];
         ss = sum16(ss);
         const float inv = __frsqrt_rn(ss / 128.0f + p.eps);
-        const float *nw = p.EV + p.evOff + (sec ? 128 : 0);
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) x[j] = v[j] * inv * nw[d0 + j];
-        const uint32_t row = p.rowOff + (live ? m : 0u);
-        const float *rp = p.RP + (size_t)row * 128;
-        if (!(p.flags & F_ROPE_HALF)) {          // interleaved pairs (2p, 2p+1), angle p
+        for (int j = 0; j < 8; j++) x[j] = v[j] * inv * nw[j];
+        const float rp[16] = {rc[0].x, rc[0].y, rc[0].z, rc[0].w, rc[1].x, rc[1].y, rc[1].z, rc[1].w,
+                              rc[2].x, rc[2].y, rc[2].z, rc[2].w, rc[3].x, rc[3].y, rc[3].z, rc[3].w};
+        if (!half) {                             // interleaved pairs (2p, 2p+1), angle p
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            const float cs = rp[d0 + j], sn = rp[d0 + j + 1];
+            const float cs = rp[j], sn = rp[j + 1];
             v[j] = x[j] * cs - x[j + 1] * sn;
             v[j + 1] = x[j] * sn + x[j + 1] * cs;
           }
@@ -317,14 +338,26 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
           const bool lo = d0 < 64;
 #pragma unroll
           for (int j = 0; j < 8; j++) {
-            const int dl = (d0 + j) & 63;
-            const float cs = rp[2 * dl], sn = rp[2 * dl + 1];
+            const float cs = rp[2 * j], sn = rp[2 * j + 1];
             v[j] = lo ? x[j] * cs - y[j] * sn : x[j] * cs + y[j] * sn;
           }
         }
+#pragma unroll
+        for (int q = 0; q < 4; q++) rc[q] = rn[q];
       }
       if (live) store_f16x8(p.Y, ((size_t)hd * p.Ltot + p.rowOff + m) * 128 + d0, v, 8);
-      continue;
+    }
+    return;
+  }
+  for (int r0 = 0; r0 < R; r0 += RPP) {
+    const int r = r0 + (tid >> 4);
+    const uint32_t m = mB + r;
+    const bool live = r < R && m < p.M;            // whole 16-lane groups agree, so the shuffles below are safe
+    float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < R) {
+      const f32x4 *src = (const f32x4 *)(C + r * ldc + g * 8);
+      f32x4 a0 = src[0], a1 = src[1];
+      v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w; v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
     }
     if (epi == E_ONORMGATE) {                                                      // gemm.js:227-232
       float ss = 0.0f;

@@ -520,28 +520,37 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
     }
   };
 
+  // X' of the slice for the rows < M only (the MFMA A reads of rows past M take zeros instead); one thread per
+  // (row, unit) task stages the unit's chunks and (q4 / q8) its sums of the unscaled X' over the low / high positions
+  // -> (G1, G2); q4: the high-nibble positions (odd pair slots) are stored as x / 16. The chunks of the first XT
+  // tasks of every thread (all of them for K <= 4096 and 16 rows) are loaded before the ring: loads return in issue
+  // order, so X loaded behind the ring would wait for its HBM units, with the ring then idle until the staging ends.
+  constexpr int CPT = UK / 8, XT = 16 / CPT;
+  const uint32_t ng = KS / UK, Mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT, ntask = Mr * ng;
+  u32x4 xr[XT][CPT];
+#pragma unroll
+  for (int i = 0; i < XT; i++) {
+    const uint32_t t = tid + i * GV_NT, m = t / ng, g = t - m * ng;
+#pragma unroll
+    for (int q = 0; q < CPT; q++)
+      xr[i][q] = t < ntask ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q) : (u32x4){0u, 0u, 0u, 0u};
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   MUnit<WE> ring[PF];
 #pragma unroll
   for (int j = 0; j < PF; j++)
     if ((uint32_t)j < nuw) load(ring[j], u0 + j);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // X' of the slice -> LDS for the rows < M only (the MFMA A reads of rows past M take zeros instead); one thread per
-  // (row, unit) stages the unit's chunks and its sums of the unscaled X' over the low / high positions -> (G1, G2);
-  // q4: the high-nibble positions (odd pair slots) are stored as x / 16
-  const uint32_t nb = KS / 8, ng = KS / UK, Mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
-  if constexpr (WE == W_F16) {
-    for (uint32_t t = tid; t < Mr * nb; t += GV_NT) {
-      uint32_t m = t / nb, kq = t - m * nb;
-      *(u32x4 *)(sX + m * KSM + 8 * kq) = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq);
-    }
-  } else {
-    const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
-    for (uint32_t t = tid; t < Mr * ng; t += GV_NT) {
-      uint32_t m = t / ng, g = t - m * ng;
-      float lo = 0.0f, hi = 0.0f;
+  const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+  auto stage = [&](uint32_t t, const u32x4 *xin) __attribute__((always_inline)) {
+    const uint32_t m = t / ng, g = t - m * ng;
+    float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-      for (int q = 0; q < UK / 8; q++) {
-        u32x4 xv = xperm<WE>(xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q));
+    for (int q = 0; q < CPT; q++) {
+      u32x4 xv = xperm<WE>(xin[q]);
+      if constexpr (WE != W_F16) {
         const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
         lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
         hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
@@ -549,11 +558,23 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
           xv.y = as_u(b * r16);
           xv.w = as_u(d * r16);
         }
-        *(u32x4 *)(sX + m * KSM + g * UK + 8 * q) = xv;
       }
-      if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
-      else sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
+      *(u32x4 *)(sX + m * KSM + g * UK + 8 * q) = xv;
     }
+    if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
+    else if constexpr (WE == W_Q8) sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
+  };
+#pragma unroll
+  for (int i = 0; i < XT; i++) {
+    const uint32_t t = tid + i * GV_NT;
+    if (t < ntask) stage(t, xr[i]);
+  }
+  for (uint32_t t = tid + XT * GV_NT; t < ntask; t += GV_NT) {
+    u32x4 xin[CPT];
+    const uint32_t m = t / ng, g = t - m * ng;
+#pragma unroll
+    for (int q = 0; q < CPT; q++) xin[q] = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q);
+    stage(t, xin);
   }
   __syncthreads();
 
