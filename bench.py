@@ -242,8 +242,20 @@ def dit_attn(dev):
                     4.0 * L * L * 128 * H, 4 * H * L * 128 * 2, L, args, [q, k, v, o], kind="attn")
 
 
+def hbm_ceiling(dev):
+    """the measured HBM read ceiling for the headline: a plain streaming read (p0k_stream_read_probe, nothing computed or
+    stored) of as many bytes as the q4 decode's weights (73,400,320), rotated over the same number of copies"""
+    nbytes = 28672 // 64 * (4096 // 32) * 1280
+    copies = max(4, -(-(2 * MALL) // nbytes))
+    bufs = [dev.buffer(nbytes) for _ in range(copies)]
+    sink = dev.buffer(16)
+    args = [{"buf": b, "bytes": nbytes, "sink": sink} for b in bufs]
+    return Workload("hbm_read_ceiling_73MB", "plain streaming read of the decode's weight bytes (ceiling probe)", "hbm", 0.0,
+                    nbytes, 1, args, bufs + [sink], {"weight_copies": copies}, kind="probe")
+
+
 BUILDERS = {
-    "decode1": lambda d: decode_q4(d, 1), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
+    "decode1": lambda d: decode_q4(d, 1), "hbm_ceiling": hbm_ceiling, "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
     "decode2": lambda d: decode_q4(d, 2), "decode8": lambda d: decode_q4(d, 8),
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
@@ -260,6 +272,9 @@ def time_workload(dev, wl, steps, warmup):
         run = dev.attention_raw
         for s in structs:
             p0k._chk(L.p0k_attention_check(C.byref(s)))
+    elif wl.kind == "probe":
+        structs = wl.args
+        run = lambda a: dev.stream_read_probe(a["buf"], a["bytes"], a["sink"])   # noqa: E731
     elif wl.kind == "rowstats":
         structs = wl.args
         run = lambda a: dev.rowstats(a["x"], a["rows"], a["cols"], a["mode"], a["eps"], a["st"])   # noqa: E731
@@ -460,6 +475,11 @@ def main():
                           "cores": cores, "kind": "port",
                           "sample": f"{cpu['sample']}; oracle/cpu_ref.mjs on Node {cpu['node']}, one thread of "
                                     f"{cpu['host_cores']} host cores ({cpu['cpu_model']})"} if cpu else None),
+        "measured_ceiling": ({"what": "plain streaming read of the headline's weight bytes, same launch shape and "
+                                      "graph timing (p0k_stream_read_probe)", "ms_per_call": results["hbm_ceiling"]["ms_per_call"],
+                              "gbps": results["hbm_ceiling"]["gbps"],
+                              "headline_vs_ceiling": round(results["hbm_ceiling"]["ms_per_call"] / head["ms_per_call"], 4)}
+                             if "hbm_ceiling" in results and head is results.get("decode1") else None),
         "device": info["name"],
         "workloads": list(results.values()),
         "wall_ms_per_step": round(hw.get("ms_per_call", 0), 5),

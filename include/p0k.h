@@ -225,6 +225,12 @@ int p0k_gn_finalize(p0k_ctx *ctx, const p0k_gn_args *a);
 /* groupnormStats(gpu, a)         src/ops/misc.js:106   partial rows of the whole tensor, then finalize */
 int p0k_groupnorm_stats(p0k_ctx *ctx, const p0k_gn_args *a);
 
+/* ---- measurement: the HBM read ceiling (no counterpart in the reference). Reads `bytes` of a live buffer with
+ *      `blocks` 512-thread workgroups (0 = 7/8 of the CUs, the decode GEMV's grid for 28672 weight rows), 16-byte
+ *      loads, nothing stored (sink: a live 4-byte buffer the kernel may write); the time per call is what the decode
+ *      GEMV's algorithmic bytes are compared with. */
+int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks);
+
 /* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
  *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */
 uint64_t p0k_tensor_bytes(int enc, uint32_t rows, uint32_t cols);

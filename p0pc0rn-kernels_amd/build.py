@@ -19,7 +19,7 @@ LIB = os.path.join(PKG, "libp0k.so")
 ADDON = os.path.join(PKG, "node", "p0k.node")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["p0k_gemm_mfma.hip", "p0k_gemm_dma.hip", "p0k_gemv.hip", "p0k_rowstats.hip", "p0k_stats.hip", "p0k_attention.hip", "p0k_runtime.cpp", "p0k_check.cpp", "p0k_pack.cpp"]
+SOURCES = ["p0k_gemm_mfma.hip", "p0k_gemm_dma.hip", "p0k_gemv.hip", "p0k_rowstats.hip", "p0k_stats.hip", "p0k_attention.hip", "p0k_probe.hip", "p0k_runtime.cpp", "p0k_check.cpp", "p0k_pack.cpp"]
 HIP_FLAGS = [
     "-x", "hip", "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
     # packed fp32 instructions stay off: ordinary float code only (v_pk_*_f32 are never emitted)

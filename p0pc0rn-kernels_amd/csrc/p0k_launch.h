@@ -48,4 +48,6 @@ hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, flo
 hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);
 hipError_t launch_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma,
                               const float *beta, float *ab, hipStream_t s);
+// the HBM read ceiling probe: reads bytes / 16 16-byte words of buf with `blocks` 512-thread workgroups
+hipError_t launch_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, unsigned blocks, hipStream_t s);
 }  // namespace p0k

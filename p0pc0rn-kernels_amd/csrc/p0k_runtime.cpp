@@ -597,6 +597,18 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
   return P0K_OK;
 }
 
+int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks) {
+  if (!c) return set_err(P0K_E_ARG, "stream_read_probe: NULL context");
+  int r;
+  if ((r = check_live(c, buf, bytes, "stream_read_probe", "buf")) || (r = check_live(c, sink, 4, "stream_read_probe", "sink")))
+    return r;
+  if (((uintptr_t)buf & 15u) != 0) return set_err(P0K_E_ARG, "stream_read_probe: buf must be 16-byte aligned");
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_stream_read(buf, bytes, sink, blocks ? blocks : c->tune.cus * 7u / 8u, c->stream);
+  if (e != hipSuccess) return hip_err(e, "stream_read_probe launch");
+  return P0K_OK;
+}
+
 uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
 
 static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {

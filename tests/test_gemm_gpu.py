@@ -446,3 +446,18 @@ def test_graph_survives_workspace_growth(dev):
     finally:
         for b in list(d.values()) + list(db.values()):
             dev.free(b)
+
+
+def test_stream_read_probe(dev):
+    """the HBM read-ceiling probe runs on a live buffer and refuses foreign or misaligned ranges"""
+    b, sink = dev.buffer(1 << 20), dev.buffer(16)
+    try:
+        dev.stream_read_probe(b, 1 << 20, sink)
+        dev.done()
+        with pytest.raises(p0k.P0kError, match="size exceeds"):
+            dev.stream_read_probe(b, 2 << 20, sink)
+        with pytest.raises(p0k.P0kError):
+            p0k._chk(p0k.lib().p0k_stream_read_probe(dev.ctx, b.ptr + 4, 1024, sink.ptr, 0))
+    finally:
+        dev.free(b)
+        dev.free(sink)
