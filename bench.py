@@ -20,6 +20,10 @@ fp32 weights, with the same prologue / epilogue formulas; oracle/cpu_ref.mjs) ti
 on a bounded sample: for the headline, whole M = 1 calls repeated for about 10 s; for the other workloads one call's
 weight decode plus a few rows of M, scaled linearly in M (the cost is exactly linear in M).
 
+    python bench.py --mfma-ceiling
+
+the matrix-core issue ceiling: how many VALU instructions per 32x32x16 MFMA a loop can hide (p0k_mfma_valu_probe).
+
     python bench.py --copy-calib
 
 runs only a plain device-to-device copy of 1 GiB, 5 times (torch's copy kernel): the reference workload for scaling the
@@ -403,6 +407,31 @@ def copy_calib(nbytes=1 << 30, reps=5):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}), flush=True)
 
 
+def mfma_ceiling(dev):
+    """`--mfma-ceiling`: FLOP rate of 8 independent 32x32x16 fp16 MFMAs per iteration with V packed-fp16 FMAs per
+    MFMA, one and two waves per SIMD (p0k_mfma_valu_probe), timed with events on the library's stream"""
+    sink = dev.buffer(16)
+    cus, iters, rows = dev.cus(), 2000, []
+    for wps in (1, 2):
+        for v in (0, 2, 4, 6, 8, 10, 12):
+            dev.mfma_valu_probe(v, wps, 10, sink)
+            dev.done()
+            e0, e1 = dev.event(), dev.event()
+            dev.record(e0)
+            dev.mfma_valu_probe(v, wps, iters, sink)
+            dev.record(e1)
+            dev.done()
+            ms = dev.elapsed_ms(e0, e1)
+            dev.event_destroy(e0)
+            dev.event_destroy(e1)
+            flop = 32768.0 * 8 * iters * 4 * cus * wps
+            rows.append({"waves_per_simd": wps, "valu_per_mfma": v, "ms": round(ms, 4),
+                         "tflops": round(flop / ms / 1e9, 1), "frac": round(flop / ms / 1e9 / (FP16_PEAK / 1e12), 4)})
+            log(f"mfma probe waves/SIMD {wps} VALU/MFMA {v:2d}: {rows[-1]['tflops']} TFLOP/s ({rows[-1]['frac']})")
+    dev.free(sink)
+    print(json.dumps({"mfma_valu_ceiling": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -411,6 +440,7 @@ def main():
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--mfma-ceiling", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (the gemm path has no multi-GPU mode here); run with --gpus 1",
@@ -421,6 +451,10 @@ def main():
         return
     names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
     dev = p0k.Device(0)
+    if a.mfma_ceiling:
+        mfma_ceiling(dev)
+        dev.close()
+        return
     info = dev.info()
     log(f"device {info}")
     results = {}

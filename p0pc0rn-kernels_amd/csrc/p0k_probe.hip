@@ -1,4 +1,7 @@
-// p0k_probe.hip — the HBM read ceiling the decode GEMV is measured against: a plain streaming read of a buffer with
+// p0k_probe.hip — measurement kernels, not part of the gemm path: the HBM read ceiling the decode GEMV is measured
+// against, and the matrix-core issue ceiling of the MFMA GEMMs (below).
+//
+// HBM read ceiling: a plain streaming read of a buffer with
 // the GEMV's launch shape (one 512-thread workgroup per 128-column tile's worth of bytes, 16-byte non-temporal loads,
 // eight in flight per lane), nothing computed and nothing stored. Its time per call, in the same graph-replay timing
 // as the bench, is the fastest a kernel can move that many bytes from HBM in one launch on this part.
@@ -28,6 +31,59 @@ __global__ __launch_bounds__(512) void k_stream_read(const u32x4 *p, uint64_t n,
 hipError_t launch_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, unsigned blocks, hipStream_t s) {
   if (bytes < 16) return hipSuccess;
   hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(512), 0, s, (const u32x4 *)buf, bytes / 16, sink);
+  return hipGetLastError();
+}
+
+}  // namespace p0k
+
+namespace p0k {
+
+// The matrix-core issue ceiling of the GEMM kernels: every iteration issues 8 independent v_mfma_f32_32x32x16_f16 on
+// eight accumulators and V independent packed-fp16 FMAs per MFMA, interleaved one MFMA then V VALU (the GEMM loop's
+// sched_group_barrier pattern). FLOP rate against the 2.5 PFLOP/s peak, for V = 0 .. 12 and one or two waves per SIMD,
+// says how much decode work per MFMA the loop can hide.
+template <int V>
+__global__ __launch_bounds__(256) void k_mfma_valu(float *sink, int iters) {
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = (f32x16){};
+  f16x8 a = {}, b = {};
+  a[0] = (f16)(float)(threadIdx.x & 7);
+  b[1] = (f16)1.0f;
+  f16x2 v[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) v[i] = (f16x2){(f16)(float)(i + (threadIdx.x & 3)), (f16)1.0f};
+  const f16x2 m = {(f16)0.999f, (f16)0.999f}, c = {(f16)0.001f, (f16)0.001f};
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 8 * V; q++) v[q % 16] = __builtin_elementwise_fma(v[q % 16], m, c);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (V) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) s += acc[i][0] + acc[i][15];
+#pragma unroll
+  for (int i = 0; i < 16; i++) s += (float)v[i].x;
+  if (s == 1.2345f) *sink = s;              // keeps the work; practically never taken
+}
+
+hipError_t launch_mfma_valu(int valu_per_mfma, unsigned blocks, int iters, float *sink, hipStream_t s) {
+  switch (valu_per_mfma) {
+  case 0: hipLaunchKernelGGL(k_mfma_valu<0>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 2: hipLaunchKernelGGL(k_mfma_valu<2>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 4: hipLaunchKernelGGL(k_mfma_valu<4>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 6: hipLaunchKernelGGL(k_mfma_valu<6>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 8: hipLaunchKernelGGL(k_mfma_valu<8>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 10: hipLaunchKernelGGL(k_mfma_valu<10>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 12: hipLaunchKernelGGL(k_mfma_valu<12>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

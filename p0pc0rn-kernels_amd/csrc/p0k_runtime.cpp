@@ -609,6 +609,17 @@ int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t 
   return P0K_OK;
 }
 
+int p0k_mfma_valu_probe(p0k_ctx *c, int valu_per_mfma, int waves_per_simd, int iters, float *sink) {
+  if (!c) return set_err(P0K_E_ARG, "mfma_valu_probe: NULL context");
+  if (waves_per_simd < 1 || waves_per_simd > 2 || iters < 1 || valu_per_mfma < 0 || valu_per_mfma > 12 || valu_per_mfma % 2)
+    return set_err(P0K_E_ARG, "mfma_valu_probe: waves_per_simd 1 or 2, iters > 0, valu_per_mfma even in 0..12");
+  if (int r = check_live(c, sink, 4, "mfma_valu_probe", "sink")) return r;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_mfma_valu(valu_per_mfma, c->tune.cus * (unsigned)waves_per_simd, iters, sink, c->stream);
+  if (e != hipSuccess) return hip_err(e, "mfma_valu_probe launch");
+  return P0K_OK;
+}
+
 uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
 
 static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {

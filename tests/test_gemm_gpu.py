@@ -461,3 +461,17 @@ def test_stream_read_probe(dev):
     finally:
         dev.free(b)
         dev.free(sink)
+
+
+def test_mfma_valu_probe(dev):
+    """the matrix-core issue probe runs and refuses out-of-range settings"""
+    sink = dev.buffer(16)
+    try:
+        dev.mfma_valu_probe(4, 2, 3, sink)
+        dev.done()
+        with pytest.raises(p0k.P0kError, match="waves_per_simd"):
+            dev.mfma_valu_probe(3, 2, 3, sink)
+        with pytest.raises(p0k.P0kError, match="waves_per_simd"):
+            dev.mfma_valu_probe(4, 3, 3, sink)
+    finally:
+        dev.free(sink)
