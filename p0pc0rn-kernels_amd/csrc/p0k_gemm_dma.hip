@@ -34,7 +34,7 @@ namespace p0k {
 
 namespace {
 
-constexpr int DBK = 64, DLDC = 128 + 4;
+constexpr int DBK = 64;
 
 // NWV waves laid out WGM x (NWV / WGM): 4 as 2 x 2, 8 as 2 x 4 (two waves per SIMD), or 4 as 1 x 4 (WGM = 1: one
 // wave per SIMD, each over all TBM rows, so a decoded weight fragment feeds TBM / 32 MFMAs)
@@ -60,7 +60,11 @@ struct DT {
   static constexpr bool TWO = NWV == 4 && WGM == 2 && 4 * STAGE <= 160 * 1024 && TBM * TBN < 256 * 256;  // two WGs per CU
   static constexpr int BUDGET = TWO ? 80 * 1024 : 160 * 1024;
   static constexpr int S = 3 * STAGE <= BUDGET ? 3 : 2;
-  static constexpr int SMEM_C = 128 * DLDC * 4;
+  // the epilogue's fp32 staging: with one workgroup per CU the whole LDS is free after the K loop, so 128 rows of the
+  // full tile width (or the whole 256 x 128 tile) go through it at once; two workgroups per CU keep 128 x 128 quadrants
+  static constexpr bool WIDE = !TWO;
+  static constexpr int CW = WIDE ? TBN : 128, CR = WIDE ? (TBN == 128 ? TBM : 128) : 128, CLD = CW + 4;
+  static constexpr int SMEM_C = CR * CLD * 4;
   static constexpr int SMEM = S * STAGE > SMEM_C ? S * STAGE : SMEM_C;
   static_assert(SMEM <= BUDGET, "LDS budget");
   static constexpr int WGN = NWV / WGM;                                        // waves along N
@@ -458,31 +462,34 @@ __attribute__((amdgpu_waves_per_eu((DT<WE, TBM, TBN, NWV, WGM>::OCC), (DT<WE, TB
   wait_lgkm0();
   stage_barrier();
 
-  // ---- accumulators -> LDS one 128 x 128 quadrant at a time (32x32 layout: lane l, register r -> row
-  //      8 (r / 4) + 4 (l / 32) + r % 4, column l % 32), then the epilogue
+  // ---- accumulators -> LDS, CR x CW at a time (32x32 layout: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4,
+  //      column l % 32), then the epilogue on each 128-column part of it (no barrier between the parts: they only read)
   float *sC = (float *)smem;
+  constexpr int CLD = T::CLD;
 #pragma unroll
-  for (int v = 0; v < TBM / 128; v++)
+  for (int v = 0; v < TBM / T::CR; v++)
 #pragma unroll
-    for (int h = 0; h < TBN / 128; h++) {
-      // the wave's 32 x 32 blocks that lie in this quadrant (a 1 x 4 layout's wave spans both row quadrants)
-      const int r0 = wm * WTM - v * 128, c0 = wn * WTN - h * 128;
+    for (int h = 0; h < TBN / T::CW; h++) {
+      // the wave's 32 x 32 blocks that lie in this part (a 1 x 4 layout's wave spans both row halves)
+      const int r0 = wm * WTM - v * T::CR, c0 = wn * WTN - h * T::CW;
 #pragma unroll
       for (int i = 0; i < BI; i++)
 #pragma unroll
         for (int j = 0; j < BJ; j++) {
           const int br = r0 + i * 32, bc2 = c0 + j * 32;
-          if (br >= 0 && br < 128 && bc2 >= 0 && bc2 < 128) {
+          if (br >= 0 && br < T::CR && bc2 >= 0 && bc2 < T::CW) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
               const int row = br + 8 * (r >> 2) + 4 * hh + (r & 3);
-              sC[row * DLDC + bc2 + l32] = acc[i][j][r];
+              sC[row * CLD + bc2 + l32] = acc[i][j][r];
             }
           }
         }
       __syncthreads();
-      epilogue<T::NT>(p, sC, DLDC, 128, mB + v * 128, nB + h * 128, tid);
-      if (v + 1 < TBM / 128 || h + 1 < TBN / 128) __syncthreads();
+#pragma unroll
+      for (int q = 0; q < T::CW / 128; q++)
+        epilogue<T::NT>(p, sC + q * 128, CLD, T::CR, mB + v * T::CR, nB + h * T::CW + q * 128, tid);
+      if (v + 1 < TBM / T::CR || h + 1 < TBN / T::CW) __syncthreads();
     }
 }
 
