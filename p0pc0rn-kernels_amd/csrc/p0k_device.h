@@ -280,6 +280,8 @@ __device__ void epilogue(const Params &p, const float *C, int ldc, int R, uint32
   if (epi == E_HEADS) {                                                            // gemm.js:216-253
     // Q / K heads: RMSNorm over the head's 128 columns, the section's norm weights (loaded once here), RoPE from the
     // table row of each output row (prefetched one pass ahead, so only the first pass waits for its loads); V raw
+    // a tile reaching past N covers heads that do not exist (N is a multiple of 128): nothing to write for them
+    if (nB >= p.N) return;
     const uint32_t hd = nB >> 7;
     const int sec = hd < p.Hq ? 0 : (hd < p.Hq + p.Hkv ? 1 : 2);
     const int d0 = g * 8;

@@ -515,7 +515,14 @@ hipError_t launch_dma_we(const Params &p, unsigned bm, unsigned bn, unsigned cus
     return launch_dma_one<WE, XG, 256, 128, 8>(p, s);
   }
   if (bm == 128 && bn == 256) return launch_dma_one<WE, XG, 128, 256>(p, s);
-  if (bm == 128 && bn == 128) return launch_dma_one<WE, XG, 128, 128>(p, s);
+  if (bm == 128 && bn == 128) {
+    // q4 with at most one tile per CU: 8 waves (2 x 4, 64 x 32 each, two per SIMD) instead of 4 at one per SIMD
+    if constexpr (WE == W_Q4) {
+      const uint64_t tiles = (uint64_t)((p.M + 127) / 128) * ((p.N - p.nbase + 127) / 128);
+      if (dma_wgs(WE, 128, 128, tiles, cus) == 1) return launch_dma_one<WE, XG, 128, 128, 8>(p, s);
+    }
+    return launch_dma_one<WE, XG, 128, 128>(p, s);
+  }
   return hipErrorInvalidValue;
 }
 
@@ -587,6 +594,7 @@ hipError_t launch_xprep(const Params &p, int xm, uint16_t *xp, hipStream_t s) {
 unsigned dma_wgs(int we, unsigned m, unsigned n, uint64_t tiles, unsigned cus) {
   if (m == 256 && n == 256) return 1;
   if (m == 256 && (we != W_Q4 || tiles <= cus)) return 1;           // 8 waves
+  if (m == 128 && n == 128 && we == W_Q4 && tiles <= cus) return 1;   // 8 waves
   if (we == W_F16) return m == 128 && n == 128 ? (DT<W_F16, 128, 128>::WGS) : (DT<W_F16, 128, 256>::WGS);
   if (we == W_Q4) return m == 128 && n == 128 ? DT<W_Q4, 128, 128>::WGS : (m == 128 ? DT<W_Q4, 128, 256>::WGS : DT<W_Q4, 256, 128>::WGS);
   return m == 128 && n == 128 ? DT<W_Q8, 128, 128>::WGS : (m == 128 ? DT<W_Q8, 128, 256>::WGS : DT<W_Q8, 256, 128>::WGS);
@@ -617,7 +625,10 @@ void dma_tile(uint32_t M, uint32_t N, int we, int xg, unsigned cus, unsigned *bm
     const double useful = (double)M * N / ((double)c.m * c.n * rounds * slots);
     // q4 256 x 128 with 8 waves (a grid of one tile per CU at most): 2048 x 4096 x 4096 in 87.7 us against 143.7 for
     // twice the work at 256 x 256
-    const double rate = (we == W_Q4 && c.m == 256 && c.n == 128 && tiles <= cus) ? 0.80 : c.rate;
+    double rate = (we == W_Q4 && c.m == 256 && c.n == 128 && tiles <= cus) ? 0.80 : c.rate;
+    // q4 128 x 128 with 8 waves (at most one tile per CU): DiT QKV's last 1024 columns as 256 such tiles instead of
+    // 128 of 256 x 128 on half the CUs, 272 -> 265 us per call
+    if (we == W_Q4 && c.m == 128 && c.n == 128 && tiles <= cus) rate = 0.6;
     const double score = rate * useful;
     if (score > best + 1e-9) { best = score; *bm = c.m; *bn = c.n; }
   }

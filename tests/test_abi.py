@@ -168,7 +168,8 @@ def test_product_encoders_match_the_oracle(enc, rows, K):
 
 @pytest.mark.parametrize("enc,M,N,tile", [("f16", 4096, 4096, (256, 256)), ("q8g64s.t64", 2048, 4096, (256, 128)),
                                           ("q4g32a.t64", 4096, 9216, (256, 256)), ("q4g32a.t64", 2048, 4096, (256, 128)),
-                                          ("q8g64s.t64", 8192, 8192, (256, 256)), ("f16", 17, 256, (128, 256))])
+                                          ("q8g64s.t64", 8192, 8192, (256, 256)), ("f16", 17, 256, (128, 256)),
+                                          ("q4g32a.t64", 1024, 4096, (128, 128))])
 def test_dma_tile_choice(enc, M, N, tile):
     """The load-to-LDS kernel's tile: 256-row tiles for quantised weights while the grid fills the CUs (a decoded
     weight feeds four 32-row blocks), smaller tiles when the grid would leave CUs idle."""

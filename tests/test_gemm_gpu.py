@@ -475,3 +475,31 @@ def test_mfma_valu_probe(dev):
             dev.mfma_valu_probe(4, 3, 3, sink)
     finally:
         dev.free(sink)
+
+
+@pytest.mark.parametrize("kernel", ["mfma_dma", "mfma"])
+def test_heads_tiles_past_n_write_nothing(dev, kernel, monkeypatch):
+    """A heads call whose last column tile reaches past N (3 heads of 128 in tiles 256 wide) must not write the
+    heads that do not exist: the bytes after the output's stated size stay as they were, for every tile shape."""
+    c = make_case(enc="f16", epi="heads", M=70, N=384, K=256, Hq=1, Hkv=1, Ltot=70, seed=95)
+    want = c.run_oracle()
+    need = c.bufs["y"].nbytes
+    guard = np.full(64 * 1024, 0xA5, np.uint8)
+    if kernel == "mfma":
+        monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
+    for t in MFMA_TILES:
+        monkeypatch.setenv("P0K_MFMA_TILE", t)
+        banner(f"heads past N: {kernel} tile {t}")
+        d = {k: dev.upload(v) for k, v in c.bufs.items() if k != "y"}
+        d["y"] = dev.upload(np.concatenate([c.bufs["y"].view(np.uint8), guard]))
+        try:
+            a = c.args(lambda n: d[n])
+            a["y"]["size"] = need
+            assert p0k.select_tile(a)["kernel"] == kernel
+            dev.gemm(a)
+            out = dev.read(d["y"], np.uint8)
+        finally:
+            for b in d.values():
+                dev.free(b)
+        assert np.array_equal(out[need:need + guard.size], guard), f"{kernel} tile {t}: wrote past the heads output"
+        assert_close(out[:need].view(np.uint16), want, what=f"heads past N {kernel} tile {t}")
