@@ -22,7 +22,13 @@ weight decode plus a few rows of M, scaled linearly in M (the cost is exactly li
 
     python bench.py --mfma-ceiling
 
-the matrix-core issue ceiling: how many VALU instructions per 32x32x16 MFMA a loop can hide (p0k_mfma_valu_probe).
+the matrix-core ceilings: how many VALU instructions per 32x32x16 MFMA a loop can hide (p0k_mfma_valu_probe) with
+constant operands, the rate the matrix cores sustain on random operands (the clock under a full MFMA load), and the
+vendor library's plain fp16 GEMM at the configs' shapes for scale.
+
+    python bench.py --hbm-ceiling
+
+the streaming-read ceiling of the headline's 73.4 MB over several launch shapes (p0k_stream_read_probe).
 
     python bench.py --copy-calib
 
@@ -247,15 +253,18 @@ def dit_attn(dev):
                     4.0 * L * L * 128 * H, 4 * H * L * 128 * 2, L, args, [q, k, v, o], kind="attn")
 
 
-def hbm_ceiling(dev):
+def hbm_ceiling(dev, blocks=0, threads=512):
     """the measured HBM read ceiling for the headline: a plain streaming read (p0k_stream_read_probe, nothing computed or
-    stored) of as many bytes as the q4 decode's weights (73,400,320), rotated over the same number of copies"""
+    stored) of as many bytes as the q4 decode's weights (73,400,320), rotated over the same number of copies; by default
+    with the decode GEMV's grid (blocks 0: 7/8 of the CUs, 512 threads)"""
     nbytes = 28672 // 64 * (4096 // 32) * 1280
     copies = max(4, -(-(2 * MALL) // nbytes))
     bufs = [dev.buffer(nbytes) for _ in range(copies)]
     sink = dev.buffer(16)
-    args = [{"buf": b, "bytes": nbytes, "sink": sink} for b in bufs]
-    return Workload("hbm_read_ceiling_73MB", "plain streaming read of the decode's weight bytes (ceiling probe)", "hbm", 0.0,
+    args = [{"buf": b, "bytes": nbytes, "sink": sink, "blocks": blocks, "threads": threads} for b in bufs]
+    name = "hbm_read_ceiling_73MB" + (f"_{blocks}x{threads}" if blocks else "")
+    return Workload(name, f"plain streaming read of the decode's weight bytes (ceiling probe, grid "
+                          f"{blocks or 'GEMV'} x {threads} threads)", "hbm", 0.0,
                     nbytes, 1, args, bufs + [sink], {"weight_copies": copies}, kind="probe")
 
 
@@ -279,7 +288,7 @@ def time_workload(dev, wl, steps, warmup):
             p0k._chk(L.p0k_attention_check(C.byref(s)))
     elif wl.kind == "probe":
         structs = wl.args
-        run = lambda a: dev.stream_read_probe(a["buf"], a["bytes"], a["sink"])   # noqa: E731
+        run = lambda a: dev.stream_read_probe(a["buf"], a["bytes"], a["sink"], a["blocks"], a["threads"])   # noqa: E731
     elif wl.kind == "rowstats":
         structs = wl.args
         run = lambda a: dev.rowstats(a["x"], a["rows"], a["cols"], a["mode"], a["eps"], a["st"])   # noqa: E731
@@ -407,29 +416,93 @@ def copy_calib(nbytes=1 << 30, reps=5):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}), flush=True)
 
 
+def mfma_probe_rate(dev, sink, v, wps, iters, rnd):
+    """one timed launch of p0k_mfma_valu_probe (after a short untimed one): (ms, TFLOP/s, fraction of the peak)"""
+    dev.mfma_valu_probe(v, wps, 10, sink, rnd)
+    dev.done()
+    e0, e1 = dev.event(), dev.event()
+    dev.record(e0)
+    dev.mfma_valu_probe(v, wps, iters, sink, rnd)
+    dev.record(e1)
+    dev.done()
+    ms = dev.elapsed_ms(e0, e1)
+    dev.event_destroy(e0)
+    dev.event_destroy(e1)
+    flop = 32768.0 * 8 * iters * 4 * dev.cus() * wps
+    return ms, round(flop / ms / 1e9, 1), round(flop / ms / 1e9 / (FP16_PEAK / 1e12), 4)
+
+
 def mfma_ceiling(dev):
     """`--mfma-ceiling`: FLOP rate of 8 independent 32x32x16 fp16 MFMAs per iteration with V packed-fp16 FMAs per
-    MFMA, one and two waves per SIMD (p0k_mfma_valu_probe), timed with events on the library's stream"""
+    MFMA, one and two waves per SIMD (p0k_mfma_valu_probe), timed with events on the library's stream; first with
+    sparse constant operands (the issue rate), then with pseudo-random operands over about 50 ms per launch (the rate
+    the part sustains on real data: the matrix cores' power draw sets the clock). Last, for scale, the vendor library's
+    plain fp16 GEMM (torch.matmul -> hipBLASLt, no dequant, no prologue / epilogue) at the configs' shapes."""
     sink = dev.buffer(16)
-    cus, iters, rows = dev.cus(), 2000, []
-    for wps in (1, 2):
-        for v in (0, 2, 4, 6, 8, 10, 12):
-            dev.mfma_valu_probe(v, wps, 10, sink)
-            dev.done()
-            e0, e1 = dev.event(), dev.event()
-            dev.record(e0)
-            dev.mfma_valu_probe(v, wps, iters, sink)
-            dev.record(e1)
-            dev.done()
-            ms = dev.elapsed_ms(e0, e1)
-            dev.event_destroy(e0)
-            dev.event_destroy(e1)
-            flop = 32768.0 * 8 * iters * 4 * cus * wps
-            rows.append({"waves_per_simd": wps, "valu_per_mfma": v, "ms": round(ms, 4),
-                         "tflops": round(flop / ms / 1e9, 1), "frac": round(flop / ms / 1e9 / (FP16_PEAK / 1e12), 4)})
-            log(f"mfma probe waves/SIMD {wps} VALU/MFMA {v:2d}: {rows[-1]['tflops']} TFLOP/s ({rows[-1]['frac']})")
+    rows = []
+    for rnd, iters, vs in ((False, 2000, (0, 2, 4, 6, 8, 10, 12)), (True, 40000, (0, 4, 6, 8))):
+        for wps in (1, 2):
+            for v in vs:
+                ms, tf, fr = mfma_probe_rate(dev, sink, v, wps, iters // wps, rnd)
+                rows.append({"operands": "random" if rnd else "constant", "waves_per_simd": wps, "valu_per_mfma": v,
+                             "ms": round(ms, 4), "tflops": tf, "frac": fr})
+                log(f"mfma probe {rows[-1]['operands']:8s} waves/SIMD {wps} VALU/MFMA {v:2d}: {tf} TFLOP/s ({fr})")
     dev.free(sink)
-    print(json.dumps({"mfma_valu_ceiling": rows}), flush=True)
+    # the library yardstick runs in a child process: torch's HIP runtime does not share this process's device
+    lib = []
+    try:
+        out = subprocess.run([sys.executable, os.path.abspath(__file__), "--library-gemm"], capture_output=True, text=True,
+                             timeout=300)
+        sys.stderr.write(out.stderr)
+        lib = json.loads(out.stdout.strip().splitlines()[-1])["library_fp16_gemm"] if out.returncode == 0 else []
+    except (OSError, subprocess.TimeoutExpired, ValueError, IndexError, KeyError) as e:
+        log(f"library yardstick failed: {e}")
+    print(json.dumps({"mfma_valu_ceiling": rows, "library_fp16_gemm": lib}), flush=True)
+
+
+def library_gemm():
+    """`--library-gemm`: the vendor library's plain fp16 GEMM (torch.matmul -> hipBLASLt; no dequant, no prologue or
+    epilogue) at the configs' GEMM shapes, N(0,1) x 0.02 N(0,1) operands, timed with torch events"""
+    import torch
+    lib = []
+    for (m, n, k, what) in ((2048, 4096, 4096, "configs[2] shape"), (4096, 9216, 3072, "DiT QKV shape"),
+                            (4096, 24576, 3072, "DiT up shape (weight rows)"), (4096, 4096, 4096, "4096^3")):
+        g = torch.Generator(device="cuda").manual_seed(7)
+        a = torch.randn(m, k, device="cuda", dtype=torch.float16, generator=g)
+        b = torch.randn(n, k, device="cuda", dtype=torch.float16, generator=g) * 0.02
+        for _ in range(3):
+            torch.matmul(a, b.t())
+        torch.cuda.synchronize()
+        reps = max(5, int(2e13 // (2 * m * n * k)))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch.matmul(a, b.t())
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        tf = 2.0 * m * n * k / ms / 1e9
+        lib.append({"what": what, "M": m, "N": n, "K": k, "ms": round(ms, 5), "tflops": round(tf, 1),
+                    "frac": round(tf * 1e12 / FP16_PEAK, 4)})
+        log(f"torch.matmul fp16 {m}x{n}x{k} ({what}): {ms * 1e3:.1f} us, {tf:.0f} TFLOP/s ({lib[-1]['frac']})")
+    print(json.dumps({"library_fp16_gemm": lib}), flush=True)
+
+
+def hbm_ceiling_sweep(dev, steps, warmup):
+    """`--hbm-ceiling`: the streaming-read ceiling of the headline's 73.4 MB over several launch shapes, in the bench's
+    graph timing: how much of the HBM peak one launch of that many bytes can reach on this part, whatever its grid"""
+    rows = []
+    for blocks, threads in ((0, 512), (256, 512), (512, 512), (512, 256), (1024, 256), (2048, 256)):
+        wl = hbm_ceiling(dev, blocks, threads)
+        ms, _, _, dist = time_workload(dev, wl, steps, warmup)
+        rows.append({"blocks": blocks or dev.cus() * 7 // 8, "threads": threads, "ms_per_call": round(ms, 5),
+                     "gbps": round(wl.algo_bytes / ms / 1e6, 1), "frac": round(wl.algo_bytes / (ms * 1e-3) / HBM_PEAK, 4),
+                     "median_ms": dist["median"] if dist else None})
+        log(f"stream read {rows[-1]['blocks']} x {threads}: {ms * 1e3:.2f} us/call, {rows[-1]['gbps']} GB/s")
+        for b in wl.bufs:
+            dev.free(b)
+        dev.drain_pool()
+    print(json.dumps({"hbm_read_ceiling": rows}), flush=True)
 
 
 def main():
@@ -441,6 +514,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--mfma-ceiling", action="store_true")
+    ap.add_argument("--hbm-ceiling", action="store_true")
+    ap.add_argument("--library-gemm", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (the gemm path has no multi-GPU mode here); run with --gpus 1",
@@ -449,10 +524,17 @@ def main():
     if a.copy_calib:
         copy_calib()
         return
+    if a.library_gemm:
+        library_gemm()
+        return
     names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
     dev = p0k.Device(0)
     if a.mfma_ceiling:
         mfma_ceiling(dev)
+        dev.close()
+        return
+    if a.hbm_ceiling:
+        hbm_ceiling_sweep(dev, a.steps, a.warmup)
         dev.close()
         return
     info = dev.info()
@@ -472,6 +554,19 @@ def main():
         for b in wl.bufs:
             dev.free(b)
         dev.drain_pool()
+    mceil = None
+    if any(r["roofline"]["bound"] == "mfma" for r in results.values()):
+        # the matrix cores' sustained rate on random operands (two waves per SIMD, no other work), measured here: what
+        # the part holds under a full MFMA load, against which each MFMA workload's rate is also reported
+        sink = dev.buffer(16)
+        ms, tf, fr = mfma_probe_rate(dev, sink, 0, 2, 20000, True)
+        dev.free(sink)
+        mceil = {"what": "8 independent 32x32x16 fp16 MFMAs per iteration on pseudo-random operands, two waves per "
+                         "SIMD, all CUs, one launch (p0k_mfma_valu_probe)", "ms": round(ms, 3), "tflops": tf, "frac": fr}
+        log(f"mfma ceiling (random operands): {tf} TFLOP/s ({fr})")
+        for r in results.values():
+            if r["roofline"]["bound"] == "mfma":
+                r["vs_mfma_ceiling"] = round(r["tflops"] / tf, 4)
     cores = 1
     if not a.no_cpu:
         cache = {}
@@ -515,6 +610,7 @@ def main():
                               "gbps": results["hbm_ceiling"]["gbps"],
                               "headline_vs_ceiling": round(results["hbm_ceiling"]["ms_per_call"] / head["ms_per_call"], 4)}
                              if "hbm_ceiling" in results and head is results.get("decode1") else None),
+        "measured_mfma_ceiling": mceil,
         "device": info["name"],
         "workloads": list(results.values()),
         "wall_ms_per_step": round(hw.get("ms_per_call", 0), 5),

@@ -226,15 +226,17 @@ int p0k_gn_finalize(p0k_ctx *ctx, const p0k_gn_args *a);
 int p0k_groupnorm_stats(p0k_ctx *ctx, const p0k_gn_args *a);
 
 /* ---- measurement: the HBM read ceiling (no counterpart in the reference). Reads `bytes` of a live buffer with
- *      `blocks` 512-thread workgroups (0 = 7/8 of the CUs, the decode GEMV's grid for 28672 weight rows), 16-byte
- *      loads, nothing stored (sink: a live 4-byte buffer the kernel may write); the time per call is what the decode
- *      GEMV's algorithmic bytes are compared with. */
-int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks);
+ *      `blocks` workgroups of `threads` (256 or 512) threads (blocks 0 = 7/8 of the CUs, the decode GEMV's grid for
+ *      28672 weight rows), 16-byte loads, eight in flight per lane, nothing stored (sink: a live 4-byte buffer the
+ *      kernel may write); the time per call is what the decode GEMV's algorithmic bytes are compared with. */
+int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks, uint32_t threads);
 /*      the matrix-core issue ceiling (no counterpart in the reference): one 256-thread workgroup per CU per wave per
  *      SIMD (waves_per_simd 1 or 2), `iters` iterations of 8 independent 32x32x16 fp16 MFMAs each followed by
  *      valu_per_mfma (even, 0..12) independent packed-fp16 FMAs; FLOPs = 32768 * 8 * iters * 4 * CUs * waves_per_simd.
- *      How much VALU work per MFMA the GEMM loops can hide. sink: a live 4-byte buffer the kernel may write. */
-int p0k_mfma_valu_probe(p0k_ctx *ctx, int valu_per_mfma, int waves_per_simd, int iters, float *sink);
+ *      How much VALU work per MFMA the GEMM loops can hide. random_operands = 0: sparse constant operands (the issue
+ *      rate alone); 1: pseudo-random fp16 operands, distinct per lane and accumulator (the rate the matrix cores hold
+ *      on real data, whose power draw sets the clock). sink: a live 4-byte buffer the kernel may write. */
+int p0k_mfma_valu_probe(p0k_ctx *ctx, int valu_per_mfma, int waves_per_simd, int iters, int random_operands, float *sink);
 
 /* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
  *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */

@@ -1,25 +1,26 @@
 // p0k_probe.hip — measurement kernels, not part of the gemm path: the HBM read ceiling the decode GEMV is measured
 // against, and the matrix-core issue ceiling of the MFMA GEMMs (below).
 //
-// HBM read ceiling: a plain streaming read of a buffer with
-// the GEMV's launch shape (one 512-thread workgroup per 128-column tile's worth of bytes, 16-byte non-temporal loads,
-// eight in flight per lane), nothing computed and nothing stored. Its time per call, in the same graph-replay timing
-// as the bench, is the fastest a kernel can move that many bytes from HBM in one launch on this part.
+// HBM read ceiling: a plain streaming read of a buffer, by default with the GEMV's launch shape (one 512-thread
+// workgroup per 128-column tile's worth of bytes, 16-byte non-temporal loads, eight in flight per lane; 256-thread
+// workgroups and any grid size are selectable), nothing computed and nothing stored. Its time per call, in the same
+// graph-replay timing as the bench, is the fastest a kernel can move that many bytes from HBM in one launch.
 #include "p0k_device.h"
 #include "p0k_launch.h"
 
 namespace p0k {
 
-__global__ __launch_bounds__(512) void k_stream_read(const u32x4 *p, uint64_t n, uint32_t *sink) {
+template <int NT>
+__global__ __launch_bounds__(NT) void k_stream_read(const u32x4 *p, uint64_t n, uint32_t *sink) {
   constexpr int U = 8;
-  uint64_t i = (uint64_t)blockIdx.x * 512u * U + threadIdx.x;
-  const uint64_t stride = (uint64_t)gridDim.x * 512u * U;
+  uint64_t i = (uint64_t)blockIdx.x * NT * U + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * NT * U;
   uint32_t acc = 0;
   for (; i < n; i += stride) {
     u32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const uint64_t j = i + (uint64_t)u * 512u;
+      const uint64_t j = i + (uint64_t)u * NT;
       v[u] = j < n ? __builtin_nontemporal_load(p + j) : (u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
@@ -28,9 +29,11 @@ __global__ __launch_bounds__(512) void k_stream_read(const u32x4 *p, uint64_t n,
   if (acc == 0x9e3779b9u) *sink = acc;      // keeps the loads; practically never taken
 }
 
-hipError_t launch_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, unsigned blocks, hipStream_t s) {
+hipError_t launch_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, unsigned blocks, unsigned threads,
+                              hipStream_t s) {
   if (bytes < 16) return hipSuccess;
-  hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(512), 0, s, (const u32x4 *)buf, bytes / 16, sink);
+  if (threads == 256) hipLaunchKernelGGL(k_stream_read<256>, dim3(blocks), dim3(256), 0, s, (const u32x4 *)buf, bytes / 16, sink);
+  else hipLaunchKernelGGL(k_stream_read<512>, dim3(blocks), dim3(512), 0, s, (const u32x4 *)buf, bytes / 16, sink);
   return hipGetLastError();
 }
 
@@ -42,21 +45,40 @@ namespace p0k {
 // eight accumulators and V independent packed-fp16 FMAs per MFMA, interleaved one MFMA then V VALU (the GEMM loop's
 // sched_group_barrier pattern). FLOP rate against the 2.5 PFLOP/s peak, for V = 0 .. 12 and one or two waves per SIMD,
 // says how much decode work per MFMA the loop can hide.
-template <int V>
+// RND = 0: sparse constant operands (one non-zero per fragment, the issue rate alone); RND = 1: every operand a
+// distinct pseudo-random fp16 in (-2, 2) per lane and accumulator, as a GEMM on real data feeds the matrix cores
+// (their power draw, and with it the clock the part holds, depends on the operand bits).
+template <int V, int RND>
 __global__ __launch_bounds__(256) void k_mfma_valu(float *sink, int iters) {
   f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = (f32x16){};
-  f16x8 a = {}, b = {};
-  a[0] = (f16)(float)(threadIdx.x & 7);
-  b[1] = (f16)1.0f;
+  f16x8 a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (f16x8){};
+    b[i] = (f16x8){};
+    if (RND) {
+      uint32_t h = (threadIdx.x + 1u) * 2654435761u ^ (uint32_t)(i + 1) * 40503u;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        h = h * 1664525u + 1013904223u;
+        a[i][q] = (f16)((float)(int)(h >> 16 & 0xffffu) * (1.0f / 16384.0f) - 2.0f);
+        h = h * 1664525u + 1013904223u;
+        b[i][q] = (f16)((float)(int)(h >> 16 & 0xffffu) * (1.0f / 16384.0f) - 2.0f);
+      }
+    } else {
+      a[i][0] = (f16)(float)(threadIdx.x & 7);
+      b[i][1] = (f16)1.0f;
+    }
+  }
   f16x2 v[16];
 #pragma unroll
   for (int i = 0; i < 16; i++) v[i] = (f16x2){(f16)(float)(i + (threadIdx.x & 3)), (f16)1.0f};
   const f16x2 m = {(f16)0.999f, (f16)0.999f}, c = {(f16)0.001f, (f16)0.001f};
   for (int it = 0; it < iters; it++) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+    for (int i = 0; i < 8; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[i], acc[i], 0, 0, 0);
 #pragma unroll
     for (int q = 0; q < 8 * V; q++) v[q % 16] = __builtin_elementwise_fma(v[q % 16], m, c);
 #pragma unroll
@@ -73,18 +95,24 @@ __global__ __launch_bounds__(256) void k_mfma_valu(float *sink, int iters) {
   if (s == 1.2345f) *sink = s;              // keeps the work; practically never taken
 }
 
-hipError_t launch_mfma_valu(int valu_per_mfma, unsigned blocks, int iters, float *sink, hipStream_t s) {
+template <int RND>
+static hipError_t launch_mfma_valu_r(int valu_per_mfma, unsigned blocks, int iters, float *sink, hipStream_t s) {
   switch (valu_per_mfma) {
-  case 0: hipLaunchKernelGGL(k_mfma_valu<0>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 2: hipLaunchKernelGGL(k_mfma_valu<2>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 4: hipLaunchKernelGGL(k_mfma_valu<4>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 6: hipLaunchKernelGGL(k_mfma_valu<6>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 8: hipLaunchKernelGGL(k_mfma_valu<8>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 10: hipLaunchKernelGGL(k_mfma_valu<10>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
-  case 12: hipLaunchKernelGGL(k_mfma_valu<12>, dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 0: hipLaunchKernelGGL((k_mfma_valu<0, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 2: hipLaunchKernelGGL((k_mfma_valu<2, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 4: hipLaunchKernelGGL((k_mfma_valu<4, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 6: hipLaunchKernelGGL((k_mfma_valu<6, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 8: hipLaunchKernelGGL((k_mfma_valu<8, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 10: hipLaunchKernelGGL((k_mfma_valu<10, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
+  case 12: hipLaunchKernelGGL((k_mfma_valu<12, RND>), dim3(blocks), dim3(256), 0, s, sink, iters); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_mfma_valu(int valu_per_mfma, int random_operands, unsigned blocks, int iters, float *sink, hipStream_t s) {
+  return random_operands ? launch_mfma_valu_r<1>(valu_per_mfma, blocks, iters, sink, s)
+                         : launch_mfma_valu_r<0>(valu_per_mfma, blocks, iters, sink, s);
 }
 
 }  // namespace p0k

@@ -597,25 +597,26 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
   return P0K_OK;
 }
 
-int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks) {
+int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks, uint32_t threads) {
   if (!c) return set_err(P0K_E_ARG, "stream_read_probe: NULL context");
   int r;
   if ((r = check_live(c, buf, bytes, "stream_read_probe", "buf")) || (r = check_live(c, sink, 4, "stream_read_probe", "sink")))
     return r;
   if (((uintptr_t)buf & 15u) != 0) return set_err(P0K_E_ARG, "stream_read_probe: buf must be 16-byte aligned");
+  if (threads != 256 && threads != 512) return set_err(P0K_E_ARG, "stream_read_probe: threads must be 256 or 512");
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_stream_read(buf, bytes, sink, blocks ? blocks : c->tune.cus * 7u / 8u, c->stream);
+  hipError_t e = p0k::launch_stream_read(buf, bytes, sink, blocks ? blocks : c->tune.cus * 7u / 8u, threads, c->stream);
   if (e != hipSuccess) return hip_err(e, "stream_read_probe launch");
   return P0K_OK;
 }
 
-int p0k_mfma_valu_probe(p0k_ctx *c, int valu_per_mfma, int waves_per_simd, int iters, float *sink) {
+int p0k_mfma_valu_probe(p0k_ctx *c, int valu_per_mfma, int waves_per_simd, int iters, int random_operands, float *sink) {
   if (!c) return set_err(P0K_E_ARG, "mfma_valu_probe: NULL context");
   if (waves_per_simd < 1 || waves_per_simd > 2 || iters < 1 || valu_per_mfma < 0 || valu_per_mfma > 12 || valu_per_mfma % 2)
     return set_err(P0K_E_ARG, "mfma_valu_probe: waves_per_simd 1 or 2, iters > 0, valu_per_mfma even in 0..12");
   if (int r = check_live(c, sink, 4, "mfma_valu_probe", "sink")) return r;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_mfma_valu(valu_per_mfma, c->tune.cus * (unsigned)waves_per_simd, iters, sink, c->stream);
+  hipError_t e = p0k::launch_mfma_valu(valu_per_mfma, random_operands != 0, c->tune.cus * (unsigned)waves_per_simd, iters, sink, c->stream);
   if (e != hipSuccess) return hip_err(e, "mfma_valu_probe launch");
   return P0K_OK;
 }

@@ -157,8 +157,8 @@ def lib():
             "p0k_ctx_create": ([I, C.POINTER(P)], I), "p0k_ctx_destroy": ([P], None),
             "p0k_ctx_reload_env": ([P], I), "p0k_ctx_cus": ([P], I),
             "p0k_gemm_noalloc": ([P, C.POINTER(GemmArgs)], I), "p0k_gemm_noalloc_scratch_bytes": ([], U64),
-            "p0k_stream_read_probe": ([P, P, U64, P, C.c_uint32], I),
-            "p0k_mfma_valu_probe": ([P, I, I, I, P], I),
+            "p0k_stream_read_probe": ([P, P, U64, P, C.c_uint32, C.c_uint32], I),
+            "p0k_mfma_valu_probe": ([P, I, I, I, I, P], I),
             "p0k_device_info_get": ([P, C.POINTER(DeviceInfo)], I),
             "p0k_alloc": ([P, U64, C.POINTER(P)], I), "p0k_free": ([P, P], I), "p0k_drain_pool": ([P], I),
             "p0k_pool_stats_get": ([P, C.POINTER(PoolStats)], I),
@@ -378,13 +378,14 @@ class Device:
         _chk(lib().p0k_gemm_noalloc(self.ctx, C.byref(s)))
         return 2 * a["M"] * a["N"] * a["K"]
 
-    def stream_read_probe(self, buf, nbytes, sink, blocks=0):
+    def stream_read_probe(self, buf, nbytes, sink, blocks=0, threads=512):
         """the HBM read ceiling kernel: read nbytes of buf, nothing stored"""
-        _chk(lib().p0k_stream_read_probe(self.ctx, buf.ptr, int(nbytes), sink.ptr, int(blocks)))
+        _chk(lib().p0k_stream_read_probe(self.ctx, buf.ptr, int(nbytes), sink.ptr, int(blocks), int(threads)))
 
-    def mfma_valu_probe(self, valu_per_mfma, waves_per_simd, iters, sink):
+    def mfma_valu_probe(self, valu_per_mfma, waves_per_simd, iters, sink, random_operands=False):
         """the matrix-core issue ceiling kernel (see include/p0k.h)"""
-        _chk(lib().p0k_mfma_valu_probe(self.ctx, int(valu_per_mfma), int(waves_per_simd), int(iters), sink.ptr))
+        _chk(lib().p0k_mfma_valu_probe(self.ctx, int(valu_per_mfma), int(waves_per_simd), int(iters),
+                                       int(bool(random_operands)), sink.ptr))
 
     def gemm_raw(self, s):
         _chk(lib().p0k_gemm(self.ctx, C.byref(s)))

@@ -453,11 +453,14 @@ def test_stream_read_probe(dev):
     b, sink = dev.buffer(1 << 20), dev.buffer(16)
     try:
         dev.stream_read_probe(b, 1 << 20, sink)
+        dev.stream_read_probe(b, 1 << 20, sink, blocks=512, threads=256)
         dev.done()
+        with pytest.raises(p0k.P0kError, match="threads"):
+            dev.stream_read_probe(b, 1 << 20, sink, threads=1024)
         with pytest.raises(p0k.P0kError, match="size exceeds"):
             dev.stream_read_probe(b, 2 << 20, sink)
         with pytest.raises(p0k.P0kError):
-            p0k._chk(p0k.lib().p0k_stream_read_probe(dev.ctx, b.ptr + 4, 1024, sink.ptr, 0))
+            p0k._chk(p0k.lib().p0k_stream_read_probe(dev.ctx, b.ptr + 4, 1024, sink.ptr, 0, 512))
     finally:
         dev.free(b)
         dev.free(sink)
@@ -468,6 +471,7 @@ def test_mfma_valu_probe(dev):
     sink = dev.buffer(16)
     try:
         dev.mfma_valu_probe(4, 2, 3, sink)
+        dev.mfma_valu_probe(0, 1, 3, sink, random_operands=True)
         dev.done()
         with pytest.raises(p0k.P0kError, match="waves_per_simd"):
             dev.mfma_valu_probe(3, 2, 3, sink)
