@@ -173,7 +173,7 @@ int p0k_ctx_create(int device, p0k_ctx **out);
 void p0k_ctx_destroy(p0k_ctx *ctx);
 int p0k_device_info_get(p0k_ctx *ctx, p0k_device_info *out);
 /* Kernel choice reads the device's CU count and the P0K_* tuning switches of the environment (P0K_MFMA_TILE,
- * P0K_MFMA_KERNEL, P0K_DMA_TAIL, P0K_GEMV_MF, P0K_GEMV_SLICES, P0K_ATTN_BQ) once, when the context is created;
+ * P0K_MFMA_KERNEL, P0K_DMA_TAIL, P0K_GEMV_MF, P0K_GEMV_MQ4, P0K_GEMV_SLICES, P0K_ATTN_BQ) once, when the context is created;
  * p0k_ctx_reload_env reads the switches again (no counterpart in the reference, whose tuning is gpu.tune,
  * src/core/tune.js:30-36). p0k_ctx_cus: the CU count the context plans for. */
 int p0k_ctx_reload_env(p0k_ctx *ctx);

@@ -54,6 +54,7 @@ Tuning tuning_from_env(unsigned cus) {
   Tuning t;
   t.cus = cus ? cus : 256;
   if (const char *ov = getenv("P0K_GEMV_MF")) t.gemv_mf = atoi(ov) != 0;
+  if (const char *ov = getenv("P0K_GEMV_MQ4")) t.gemv_mq4 = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_GEMV_SLICES")) t.gemv_slices = (unsigned)std::max(0, atoi(ov));
   if (const char *ov = getenv("P0K_MFMA_KERNEL")) t.mfma_reg = strcmp(ov, "reg") == 0;
   if (const char *ov = getenv("P0K_MFMA_TILE")) {

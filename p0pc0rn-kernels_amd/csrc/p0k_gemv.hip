@@ -56,19 +56,19 @@ constexpr int ks_max() { return (GV_LDS * 8 / (MT * 18)) & ~1023; }
 // output element sums the element's K-quarters (in quarter order, as finish() does) and applies the epilogue, so the
 // tile needs no summing pass of its own and every thread has a few instructions of work (the 16-byte-store epilogue
 // of finish() gives 8 threads 8 outputs each per row, a long serial tail at the end of the stream).
-template <int MT>
+template <int MT, int KQ = GV_KSUB, int NT = GV_NT>
 __device__ __forceinline__ void finish_fast(const Params &p, const float *sR, uint32_t nB, int tid) {
   const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
   auto qsum = [&](uint32_t m, uint32_t c) {
     float s = sR[m * 128 + c];
 #pragma unroll
-    for (int q = 1; q < GV_KSUB; q++) s += sR[(q * MT + m) * 128 + c];
+    for (int q = 1; q < KQ; q++) s += sR[(q * MT + m) * 128 + c];
     return s;
   };
   if (p.epi == E_SWIGLU) {                                                        // gemm.js:204-210
     const uint32_t Nout = p.N >> 1;
     const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
-    for (uint32_t t = tid; t < rows * 64; t += GV_NT) {
+    for (uint32_t t = tid; t < rows * 64; t += NT) {
       const uint32_t m = t >> 6, c = t & 63, o = (nB >> 1) + c;
       if (o >= Nout) continue;
       float gt = qsum(m, 2 * c), u = qsum(m, 2 * c + 1);
@@ -77,7 +77,7 @@ __device__ __forceinline__ void finish_fast(const Params &p, const float *sR, ui
     }
     return;
   }
-  for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+  for (uint32_t t = tid; t < rows * 128; t += NT) {
     const uint32_t m = t >> 7, c = t & 127, col = nB + c;
     if (col >= p.N) continue;
     const float v = qsum(m, c);
@@ -105,14 +105,14 @@ __device__ __forceinline__ bool fast_epi(const Params &p, uint32_t S) {
 
 // After the stream: the K-quarter partials of the item are in sR as [quarter][m][128 ws columns]; sum them, meet the
 // other slices of the tile when S > 1, and run the epilogue.
-template <int MT>
+template <int MT, int KQ = GV_KSUB, int NT = GV_NT>
 __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, uint32_t *cnt, uint32_t S, uint32_t tile,
                                        uint32_t slice, uint32_t nB, int tid, uint32_t *sLast_) {
   uint32_t &sLast = *sLast_;
-  for (int t = tid; t < MT * 128; t += GV_NT) {
+  for (int t = tid; t < MT * 128; t += NT) {
     float s = sR[t];
 #pragma unroll
-    for (int q = 1; q < GV_KSUB; q++) s += sR[q * MT * 128 + t];
+    for (int q = 1; q < KQ; q++) s += sR[q * MT * 128 + t];
     sR[t] = s;
   }
   __syncthreads();
@@ -124,7 +124,7 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
     // and every thread waits for its acknowledgements before the barrier that precedes the counter update.
     const uint32_t Np = gridDim.x / S * 128u;
     const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
-    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+    for (uint32_t t = tid; t < rows * 128; t += NT) {
       uint32_t m = t >> 7, c = t & 127;
       __hip_atomic_store(part + ((size_t)slice * p.M + m) * Np + nB + c, sR[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
@@ -136,7 +136,7 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
     }
     __syncthreads();
     if (!sLast) return;
-    for (uint32_t t = tid; t < rows * 128; t += GV_NT) {
+    for (uint32_t t = tid; t < rows * 128; t += NT) {
       uint32_t m = t >> 7, c = t & 127;
       const float *src = part + (size_t)m * Np + nB + c;
       float s = 0.0f;
@@ -147,7 +147,7 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
     if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
   }
-  epilogue<GV_NT>(p, sR, 128, MT, 0u, nB, tid);
+  epilogue<NT>(p, sR, 128, MT, 0u, nB, tid);
 }
 
 template <int WE, int XM, int MT>
@@ -603,6 +603,182 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Decode on the matrix cores with q4 weights and 3..16 rows, without staging X'. The same 128-column items as above,
+// but each of the 8 waves covers all 128 columns of one K-eighth, so each X' fragment it loads serves 8 blocks of 16
+// weight rows. Per 32-k unit a wave runs ten v_mfma_f32_16x16x32_f16, every operand in registers:
+//   * lane l loads code rows l and 64 + l of the unit (16 bytes each: one 128-bit load covers 64 rows' 1 KB) and their
+//     (scale, min) words, as the one-row stream does; a 4 x 4 transpose across the four 16-lane groups (two
+//     v_permlane32_swap and two v_permlane16_swap per 64 rows) then gives lane (kc = l / 16, l16 = l % 16) code word
+//     kc of row 16 i + l16 in register i, the B fragment of block i (magic-biased in place: 1024 + q low nibbles,
+//     1024 + 16 q high), and the same swaps broadcast row 16 i + l16's (scale, min) word to it
+//   * each lane reads its A fragment, X' row l16 (rows past M repeat row M - 1, whose products land in output rows
+//     that are never stored), k = 8 kc .. 8 kc + 7 of the unit, and puts it into the pair order of the decode, the
+//     high-nibble positions scaled by 1/16. fp16 X with 16-byte rows (XL): the item's X rows are copied to LDS as
+//     they are by the load-to-LDS path (global_load_lds_dwordx4, no registers), issued before the weight ring so the
+//     copy runs under the ring's first HBM latency; rows 16 bytes longer than K, so the 16 rows one A read touches
+//     start in different banks. Otherwise (rms / lnmod prologues, unaligned X) the fragment is computed from X with
+//     the same unit's loads.
+//   * two MFMAs against constant B operands give, for every output column, -G1 = -(1024 X_lo + 64 X_hi) and
+//     G2 = X_lo + X_hi of the unit's rows; each block's MFMA starts from -G1, so it returns sum x q directly, and
+//     y += s (sum x q) + mn G2 in registers (the fp32 weight model of the stream above).
+#ifndef P0K_MQ4_NW
+#define P0K_MQ4_NW 8
+#endif
+constexpr int MQ_KQ = P0K_MQ4_NW, MQ_NT = 64 * MQ_KQ;           // waves = K parts of an item
+constexpr int MQ_XP = MF_KSM * 2 + 16;                       // LDS bytes per staged X row
+constexpr int MQ_LDS = 16 * MQ_XP > MQ_KQ * 16 * 128 * 4 ? 16 * MQ_XP : MQ_KQ * 16 * 128 * 4;
+#ifndef P0K_MQ4_PF
+#define P0K_MQ4_PF 3
+#endif
+template <int XM, bool XL>
+__global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
+  constexpr int MT = 16, PF = P0K_MQ4_PF;
+  static_assert(!XL || XM == X_F16, "X rows are copied as they are only without a prologue");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[XL ? MQ_LDS : MQ_KQ * MT * 128 * 4];
+  __shared__ uint32_t sLast;
+  float *sR = (float *)smem;                                   // after the stream: the K-eighths' partials
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, kc = lane >> 4;
+  const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
+  const uint32_t nB = tile * 128u, kb0 = slice * KS;
+  const uint32_t nu = KS / 32u, u0 = wave * nu / MQ_KQ, nuw = (wave + 1) * nu / MQ_KQ - u0;   // units of this wave
+
+  // this lane's weight rows (lane and 64 + lane of the tile): byte offsets of their code rows and (scale, min) words in
+  // the wave's first unit (32-bit: tensors of 4 GiB or more take the MFMA GEMM)
+  uint32_t woff[2], soff[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const uint32_t r = wrow(p, nB + 64 * h + lane);
+    const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5) + u0) * 1280u;
+    woff[h] = rec + (r & 63u) * 16u;
+    soff[h] = rec + 1024u + (r & 63u) * 4u;
+  }
+  const uint32_t xrow = (uint32_t)l16 < p.M ? (uint32_t)l16 : p.M - 1u;
+  const uint32_t xk0 = kb0 + u0 * 32u + (uint32_t)kc * 8u;
+
+  if constexpr (XL) {
+    // X rows [0, min(M, 16)) of the slice -> LDS, 1 KB per instruction (lane l: 16 bytes at 16 l), instruction q of
+    // the list taken by wave q % 8
+    // (a row's last instruction may reach past KS: those lanes re-read the row's first 16 bytes into the row's
+    // padding, which an LDS row of whole KB plus 16 bytes leaves room for)
+    const uint32_t mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT, cpr = (KS + 511u) / 512u, nq = mr * cpr;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)smem;
+    for (uint32_t q = (uint32_t)wave; q < nq; q += (uint32_t)MQ_KQ) {
+      const uint32_t m = q / cpr, c = q - m * cpr, k = c * 512u + 8u * (uint32_t)lane;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + m * (uint32_t)MQ_XP + c * 1024u);
+      const uint8_t *src = p.X + ((size_t)m * p.ldx + p.kx0 + kb0 + (k < KS ? k : 0u)) * 2u;
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
+    }
+  }
+
+  struct U { u32x4 code[2]; uint32_t sm[2]; u32x4 x; };
+  auto load = [&](U &u, uint32_t j) __attribute__((always_inline)) {
+    const uint32_t du = j * 1280u;
+#pragma unroll
+    for (int h = 0; h < 2; h++) u.code[h] = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[h] + du)));
+#pragma unroll
+    for (int h = 0; h < 2; h++) u.sm[h] = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[h] + du)));
+    if constexpr (!XL) u.x = xload8<XM>(p, xrow, RowCtx{0, 0, 0}, xk0 + j * 32u);
+  };
+  // the A fragment of the wave's unit j
+  const uint8_t *xs = smem + xrow * (uint32_t)MQ_XP + (u0 * 32u + (uint32_t)kc * 8u) * 2u;
+  auto xfrag = [&](const U &u, uint32_t j) __attribute__((always_inline)) -> u32x4 {
+    if constexpr (XL) return *(const u32x4 *)(xs + j * 64u);
+    else return u.x;
+  };
+
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mag = 0x64006400u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi), "+v"(mag));
+  // B of -G1: every half -1024; B of G2: 1 at the low-nibble positions (pair slots 0, 2), 16 at the high ones (1, 3)
+  const f16x8 bneg = __builtin_bit_cast(f16x8, (u32x4){0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
+  const f16x8 bg2 = __builtin_bit_cast(f16x8, (u32x4){0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});
+  const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+  const f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = z4;
+
+  auto compute = [&](const U &u, uint32_t j) __attribute__((always_inline)) {
+    u32x4 xv = xperm<W_Q4>(xfrag(u, j));
+    xv.y = as_u(as_h2(xv.y) * r16);
+    xv.w = as_u(as_h2(xv.w) * r16);
+    const f16x8 a = __builtin_bit_cast(f16x8, xv);
+    const f32x4 ng1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bneg, z4, 0, 0, 0);
+    const f32x4 g2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bg2, z4, 0, 0, 0);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      // the 4 x 4 transpose of (16-lane group, code word): word kc of row 64 h + 16 i + l16 into register i
+      uint32_t w[4];
+      {
+        const auto p02 = __builtin_amdgcn_permlane32_swap(u.code[h].x, u.code[h].z, false, false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(u.code[h].y, u.code[h].w, false, false);
+        const auto q01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+        const auto q23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+        w[0] = q01[0]; w[1] = q01[1]; w[2] = q23[0]; w[3] = q23[1];
+      }
+      // row 64 h + 16 i + l16's (scale, min) word, from lane 16 i + l16, into register i
+      uint32_t sm[4];
+      {
+        const auto t = __builtin_amdgcn_permlane32_swap(u.sm[h], u.sm[h], false, false);
+        const auto q0 = __builtin_amdgcn_permlane16_swap(t[0], t[0], false, false);
+        const auto q1 = __builtin_amdgcn_permlane16_swap(t[1], t[1], false, false);
+        sm[0] = q0[0]; sm[1] = q0[1]; sm[2] = q1[0]; sm[3] = q1[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t w8 = w[i] >> 8;
+        const u32x4 bw = (u32x4){(w[i] & mlo) | mag, (w[i] & mhi) | mag, (w8 & mlo) | mag, (w8 & mhi) | mag};
+        const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, bw), ng1, 0, 0, 0);
+        const f16x2 sm2 = as_h2(sm[i]);
+        const float s = (float)sm2.x, mn = (float)sm2.y;
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[4 * h + i][r] = fmaf(s, d[r], fmaf(mn, g2[r], acc[4 * h + i][r]));
+      }
+    }
+  };
+
+  // (a slice shorter than 8 units leaves waves idle; their ring loads stay inside the item's first unit)
+  const uint32_t nl = nuw ? nuw - 1u : 0u;
+  U ring[PF];
+#pragma unroll
+  for (int j = 0; j < PF; j++) {
+    load(ring[j], (uint32_t)j < nl ? (uint32_t)j : nl);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (XL) {
+    // the X copy is older than the ring's loads (loads complete in order): wait for it alone, then for every wave's
+    __builtin_amdgcn_s_waitcnt((4 * PF & 15) | (((4 * PF) >> 4) << 14) | 0x0f70);   // vmcnt(4 PF): 4 loads per unit
+    __syncthreads();
+  }
+  uint32_t j0 = 0;
+#pragma unroll 1
+  for (; j0 + PF <= nuw; j0 += PF) {
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      compute(ring[j], j0 + j);
+      const uint32_t nx = j0 + PF + j;
+      load(ring[j], nx < nuw ? nx : nl);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PF; j++)
+    if (j0 + j < nuw) compute(ring[j], j0 + j);
+  if constexpr (XL) __syncthreads();                           // X' is dead: the buffer takes the partials
+
+  // D[m = 4 kc + r][row 16 i + l16] of the tile's rows 64 h + ...; the K-eighths meet in LDS
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) sR[(wave * MT + 4 * kc + r) * 128 + 16 * i + l16] = acc[i][r];
+  __syncthreads();
+  if (fast_epi(p, S)) finish_fast<MT, MQ_KQ, MQ_NT>(p, sR, nB, tid);
+  else finish<MT, MQ_KQ, MQ_NT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
+}
+
 static uint32_t ks_max_of(uint32_t M, bool mf) {
   if (mf) return MF_KSM;
   return M <= 1 ? ks_max<1>() : M <= 2 ? ks_max<2>() : M <= 4 ? ks_max<4>() : M <= 8 ? ks_max<8>() : ks_max<16>();
@@ -630,10 +806,16 @@ static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t 
   return hipGetLastError();
 }
 template <int WE, int XM>
-static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s, bool mf) {
+static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s, bool mf,
+                          bool mq4) {
   if (mf) {
     if (KS > (uint32_t)MF_KSM) return hipErrorInvalidValue;
     dim3 grid(((p.N + 127) / 128) * S);
+    if (WE == W_Q4 && mq4) {
+      if (XM == X_F16 && (p.flags & F_XALIGN8)) hipLaunchKernelGGL((k_gemv_mq4<X_F16, true>), grid, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
+      else hipLaunchKernelGGL((k_gemv_mq4<XM, false>), grid, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
   }
@@ -645,23 +827,23 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
 }
 template <int WE>
 static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s,
-                          bool mf) {
+                          bool mf, bool mq4) {
   switch (xm) {
-  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf);
-  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf);
-  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf);
+  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf, mq4);
+  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf, mq4);
+  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf, mq4);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
-                       hipStream_t s, bool mf) {
+                       hipStream_t s, bool mf, bool mq4) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
   switch (we) {
-  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf);
-  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf);
-  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf);
+  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4);
+  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4);
+  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf, mq4);
   }
   return hipErrorInvalidValue;
 }

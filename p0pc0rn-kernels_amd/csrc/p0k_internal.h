@@ -15,6 +15,7 @@ struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; };
 struct Tuning {
   unsigned cus = 256;
   int gemv_mf = -1;            // P0K_GEMV_MF=0: the VALU stream for M > 1 (-1: not set)
+  bool gemv_mq4 = true;        // P0K_GEMV_MQ4=0: q4 matrix-core decode with X' staged in LDS (k_gemv_mf)
   unsigned gemv_slices = 0;    // P0K_GEMV_SLICES=n: decode K slices (0: not set)
   bool mfma_reg = false;       // P0K_MFMA_KERNEL=reg: the register-staged MFMA kernel
   unsigned tile_m = 0, tile_n = 0;   // P0K_MFMA_TILE=MxN

@@ -52,10 +52,13 @@ def oracle_rows(case, ranges, weights):
     return want
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
-def test_decode_q4_swiglu_full(dev, M):
-    """q4 N = 14336 (gate | up: 28672 weight rows), K = 4096, SwiGLU; every output row."""
-    banner(f"full-size decode M={M}")
+@pytest.mark.parametrize("M,staged", [(1, False), (4, False), (16, False), (16, True)])
+def test_decode_q4_swiglu_full(dev, M, staged, monkeypatch):
+    """q4 N = 14336 (gate | up: 28672 weight rows), K = 4096, SwiGLU; every output row. staged: the
+    matrix-core decode with X' staged in LDS before the stream (P0K_GEMV_MQ4=0) instead of k_gemv_mq4."""
+    if staged:
+        monkeypatch.setenv("P0K_GEMV_MQ4", "0")
+    banner(f"full-size decode M={M} staged={staged}")
     c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=28672, K=4096, seed=101, wscale=0.02)
     t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
     assert t["kernel"] == ("gemv" if M == 1 else "gemv_mfma")

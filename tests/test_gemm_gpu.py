@@ -135,19 +135,22 @@ def _adversarial_q8(rows, K, seed):
 
 
 @pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
-@pytest.mark.parametrize("path", ["gemv", "gemv_mfma", "mfma"])
+@pytest.mark.parametrize("path", ["gemv", "gemv_mfma", "gemv_mfma_staged", "mfma"])
 def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
-    to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream.)"""
+    to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream;
+    P0K_GEMV_MQ4=0 the q4 matrix-core decode with X' staged in LDS.)"""
     if path == "gemv":
         monkeypatch.setenv("P0K_GEMV_MF", "0")
+    if path == "gemv_mfma_staged":
+        monkeypatch.setenv("P0K_GEMV_MQ4", "0")
     rows, K = 128, 256
     wb = _adversarial_q4(rows, K, 3) if enc.startswith("q4") else _adversarial_q8(rows, K, 4)
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
     dw = dev.upload(wb)
     try:
-        M = {"gemv": 1, "gemv_mfma": 16, "mfma": K}[path]
+        M = {"gemv": 1, "gemv_mfma": 16, "gemv_mfma_staged": 16, "mfma": K}[path]
         got = np.zeros((K, rows), np.uint16)
         for k0 in range(0, K, M):
             X = np.zeros((M, K), np.float32)
