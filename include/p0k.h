@@ -228,7 +228,8 @@ int p0k_groupnorm_stats(p0k_ctx *ctx, const p0k_gn_args *a);
 /* ---- measurement: the HBM read ceiling (no counterpart in the reference). Reads `bytes` of a live buffer with
  *      `blocks` workgroups of `threads` (256 or 512) threads (blocks 0 = 7/8 of the CUs, the decode GEMV's grid for
  *      28672 weight rows), 16-byte loads, eight in flight per lane, nothing stored (sink: a live 4-byte buffer the
- *      kernel may write); the time per call is what the decode GEMV's algorithmic bytes are compared with. */
+ *      kernel may write; bytes below 4 GiB); the time per call is what the decode GEMV's algorithmic bytes are
+ *      compared with. */
 int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks, uint32_t threads);
 /*      the matrix-core issue ceiling (no counterpart in the reference): one 256-thread workgroup per CU per wave per
  *      SIMD (waves_per_simd 1 or 2), `iters` iterations of 8 independent 32x32x16 fp16 MFMAs each followed by

@@ -57,6 +57,22 @@ struct Params {
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// Streaming reads of data used once per call (the decode's weights): buffer loads at 32-bit byte offsets from a raw
+// buffer resource over the tensor, cache policy "sc0 nt" (non-temporal). They move the decode's 73 MB about 1.5 %
+// faster than global loads with the nt bit alone.
+typedef __amdgpu_buffer_rsrc_t srsrc;
+__device__ __forceinline__ srsrc stream_rsrc(const uint8_t *base) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)0xffffffff, 0x00020000);
+}
+constexpr int SC0_NT = 3;   // buffer-load cache policy bits on gfx950: 1 = sc0, 2 = nt
+__device__ __forceinline__ u32x4 sload128(srsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, SC0_NT));
+}
+__device__ __forceinline__ u32x2 sload64(srsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, SC0_NT));
+}
+__device__ __forceinline__ uint32_t sload32(srsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, SC0_NT); }
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 

@@ -37,7 +37,8 @@ constexpr int GV_KSUB = P0K_GV_KSUB, GV_NT = 2 * GV_KSUB * 64;     // 512 thread
 #ifndef P0K_GV_LDS_KB
 #define P0K_GV_LDS_KB 40
 #endif
-constexpr int GV_LDS = P0K_GV_LDS_KB * 1024;                       // X' of the slice and its group sums, then the partials
+constexpr int GV_LDS = P0K_GV_LDS_KB * 1024;
+                       // X' of the slice and its group sums, then the partials
 
 template <int WE>
 struct Unit;
@@ -180,19 +181,19 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
 
   const uint32_t sadj = 1024u - (r & 63u) * 12u;             // q4: code row -> scale word of row r in the record
+  const srsrc wr = stream_rsrc(p.W);
   auto load = [&](Unit<WE> &u, uint32_t unit) {
-    const uint32_t o = woff + unit * USTRIDE;                  // 32-bit offsets from the uniform base: no 64-bit
-    const uint8_t *src = p.W + o;                              // address temporaries in the stream loop
+    const uint32_t o = woff + unit * USTRIDE;                  // 32-bit offsets from the uniform base
     if constexpr (WE == W_Q4) {
-      u.code = __builtin_nontemporal_load((const u32x4 *)src);
-      u.sm = __builtin_nontemporal_load((const uint32_t *)(p.W + (o + sadj)));   // scale word r
+      u.code = sload128(wr, o);
+      u.sm = sload32(wr, o + sadj);                            // scale word r
     } else if constexpr (WE == W_Q8) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) u.code[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16u * i));
-      u.s = __builtin_nontemporal_load((const uint32_t *)(p.W + (o + 4096u - (r & 63u) * 64u + (r & 62u) * 2u)));
+      for (int i = 0; i < 4; i++) u.code[i] = sload128(wr, o + 16u * i);
+      u.s = sload32(wr, o + 4096u - (r & 63u) * 64u + (r & 62u) * 2u);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; i++) u.v[i] = __builtin_nontemporal_load((const u32x4 *)(src + 16 * i));
+      for (int i = 0; i < 4; i++) u.v[i] = sload128(wr, o + 16u * i);
     }
   };
 
@@ -425,20 +426,21 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   }
   constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
 
+  const srsrc wr = stream_rsrc(p.W);
   auto load = [&](MUnit<WE> &u, uint32_t unit) {
     const uint32_t du = unit * USTRIDE;
     if constexpr (WE == W_Q4) {
-      u.code = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[0] + du)));
-      u.sm = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[0] + du)));
+      u.code = sload128(wr, woff[0] + du);
+      u.sm = sload32(wr, soff[0] + du);
     } else {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       if constexpr (WE == W_Q8) {
-        u.code[i][0] = __builtin_nontemporal_load((const u32x2 *)(p.W + (woff[i] + du)));
-        u.code[i][1] = __builtin_nontemporal_load((const u32x2 *)(p.W + (woff[i] + du + 32u)));
-        u.s[i] = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[i] + du)));
+        u.code[i][0] = sload64(wr, woff[i] + du);
+        u.code[i][1] = sload64(wr, woff[i] + du + 32u);
+        u.s[i] = sload32(wr, soff[i] + du);
       } else {
-        u.v[i] = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[i] + du)));
+        u.v[i] = sload128(wr, woff[i] + du);
       }
     }
     }
@@ -674,12 +676,13 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   }
 
   struct U { u32x4 code[2]; uint32_t sm[2]; u32x4 x; };
+  const srsrc wr = stream_rsrc(p.W);
   auto load = [&](U &u, uint32_t j) __attribute__((always_inline)) {
     const uint32_t du = j * 1280u;
 #pragma unroll
-    for (int h = 0; h < 2; h++) u.code[h] = __builtin_nontemporal_load((const u32x4 *)(p.W + (woff[h] + du)));
+    for (int h = 0; h < 2; h++) u.code[h] = sload128(wr, woff[h] + du);
 #pragma unroll
-    for (int h = 0; h < 2; h++) u.sm[h] = __builtin_nontemporal_load((const uint32_t *)(p.W + (soff[h] + du)));
+    for (int h = 0; h < 2; h++) u.sm[h] = sload32(wr, soff[h] + du);
     if constexpr (!XL) u.x = xload8<XM>(p, xrow, RowCtx{0, 0, 0}, xk0 + j * 32u);
   };
   // the A fragment of the wave's unit j

@@ -4,7 +4,8 @@
 // HBM read ceiling: a plain streaming read of a buffer, by default with the GEMV's launch shape (one 512-thread
 // workgroup per 128-column tile's worth of bytes, 16-byte non-temporal loads, eight in flight per lane; 256-thread
 // workgroups and any grid size are selectable), nothing computed and nothing stored. Its time per call, in the same
-// graph-replay timing as the bench, is the fastest a kernel can move that many bytes from HBM in one launch.
+// graph-replay timing as the bench, is the fastest a kernel can move that many bytes from HBM in one launch. The
+// loads are the decode's own streaming form (sload128: buffer loads, sc0 nt).
 #include "p0k_device.h"
 #include "p0k_launch.h"
 
@@ -13,15 +14,17 @@ namespace p0k {
 template <int NT>
 __global__ __launch_bounds__(NT) void k_stream_read(const u32x4 *p, uint64_t n, uint32_t *sink) {
   constexpr int U = 8;
-  uint64_t i = (uint64_t)blockIdx.x * NT * U + threadIdx.x;
-  const uint64_t stride = (uint64_t)gridDim.x * NT * U;
+  // (n < 2^28: 32-bit byte offsets, checked on the host)
+  uint32_t i = blockIdx.x * NT * U + threadIdx.x;
+  const uint32_t stride = gridDim.x * NT * U;
+  const srsrc r = stream_rsrc((const uint8_t *)p);
   uint32_t acc = 0;
   for (; i < n; i += stride) {
     u32x4 v[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const uint64_t j = i + (uint64_t)u * NT;
-      v[u] = j < n ? __builtin_nontemporal_load(p + j) : (u32x4){0u, 0u, 0u, 0u};
+      const uint32_t j = i + u * NT;
+      v[u] = j < n ? sload128(r, j * 16u) : (u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;

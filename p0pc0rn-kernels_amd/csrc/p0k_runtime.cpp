@@ -605,6 +605,7 @@ int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t 
     return r;
   if (((uintptr_t)buf & 15u) != 0) return set_err(P0K_E_ARG, "stream_read_probe: buf must be 16-byte aligned");
   if (threads != 256 && threads != 512) return set_err(P0K_E_ARG, "stream_read_probe: threads must be 256 or 512");
+  if (bytes >= (1ull << 32)) return set_err(P0K_E_ARG, "stream_read_probe: bytes must be below 4 GiB");
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
   hipError_t e = p0k::launch_stream_read(buf, bytes, sink, blocks ? blocks : c->tune.cus * 7u / 8u, threads, c->stream);
   if (e != hipSuccess) return hip_err(e, "stream_read_probe launch");
