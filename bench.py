@@ -52,13 +52,13 @@ HBM_PEAK = 8.0e12          # B/s, MI355X published
 FP16_PEAK = 2.5e15         # FLOP/s dense fp16 MFMA, MI355X published
 MALL = 256 << 20
 
-# HBM bytes per launch from rocprofv3 counters (profiles/k_gemv_*_decode_M*.md, k_stream_read_73MB_ceiling.md): FETCH_SIZE and WRITE_SIZE in
+# HBM bytes per launch from rocprofv3 counters (profiles/k_gemv*_decode_M*.md, k_stream_read_73MB_ceiling.md): FETCH_SIZE and WRITE_SIZE in
 # KiB per dispatch, each times what the same counter reads per byte of a plain 1 GiB device copy (`--copy-calib`:
 # FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run, so the
 # figures of the last profiled build are kept here, per workload.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35989, 28), "decode_q4_swiglu_M4": (36210, 112), "decode_q4_swiglu_M16": (36604, 448),
-               "hbm_read_ceiling_73MB": (35855, 0)}
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35993, 28), "decode_q4_swiglu_M4": (36250, 112), "decode_q4_swiglu_M16": (36667, 448),
+               "hbm_read_ceiling_73MB": (35851, 0)}
 
 
 def log(msg):
