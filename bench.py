@@ -58,7 +58,11 @@ MALL = 256 << 20
 # figures of the last profiled build are kept here, per workload.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35993, 28), "decode_q4_swiglu_M4": (36250, 112), "decode_q4_swiglu_M16": (36667, 448),
-               "hbm_read_ceiling_73MB": (35851, 0)}
+               "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
+               # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
+               "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
+               "dit_qkv_q4_lnmod_heads": (132057, 98304), "dit_up_q4_geglu": (250822, 98304),
+               "conv3_128_T13x92x160": (190772, 47840), "dit_attention_24x4096": (36917, 26127)}
 
 
 def log(msg):
@@ -374,8 +378,10 @@ def roofline(wl, ms):
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                 "frac": round(ach * 1e9 / HBM_PEAK, 4), "traffic": traffic}
     ach = wl.flops / sec / 1e12
+    t = TRAFFIC_KIB.get(wl.name)
+    traffic = int((FETCH_FACTOR * t[0] + WRITE_FACTOR * t[1]) * 1024) if t else None
     return {"bound": "mfma", "achieved": round(ach, 2), "peak": FP16_PEAK / 1e12, "unit": "TFLOP/s",
-            "frac": round(ach * 1e12 / FP16_PEAK, 4), "traffic": None}
+            "frac": round(ach * 1e12 / FP16_PEAK, 4), "traffic": traffic}
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
