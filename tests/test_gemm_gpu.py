@@ -115,6 +115,31 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
         assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M} register-staged")
 
 
+# ------------------------------------------------------------------------------------------------ matrix-core decode
+DECODE_OFFSET_CASES = [
+    # 16-byte X rows with row / column offsets: the item's X rows are copied to LDS (load-to-LDS)
+    dict(enc="q4g32a.t64", epi="f16", M=5, N=320, K=384, ld_pad=8, k0=64, wk0=32, n0=8),
+    dict(enc="q4g32a.t64", epi="swiglu", M=16, N=512, K=512, ld_pad=24, k0=16, wr0=64),
+    # rows or k0 not a multiple of 8 halfs: the A fragments are read from X with each unit's loads
+    dict(enc="q4g32a.t64", epi="f16", M=3, N=192, K=256, ld_pad=4),
+    dict(enc="q4g32a.t64", epi="resadd", M=9, N=256, K=640, ld_pad=4, k0=4),
+    # a slice shorter than one unit per wave (K = 128: 4 units for 8 waves)
+    dict(enc="q4g32a.t64", epi="f32", M=12, N=256, K=128),
+]
+
+
+@pytest.mark.parametrize("kw", DECODE_OFFSET_CASES, ids=lambda k: f"M{k['M']}-K{k['K']}-pad{k.get('ld_pad', 0)}-k0{k.get('k0', 0)}")
+def test_matrix_core_decode_offsets(dev, kw):
+    """q4 decode with 3..16 rows (k_gemv_mq4): X row pitch / column offset, weight column and row offsets, output
+    column offset; both ways the kernel gets its A fragments (LDS copy of aligned X rows, per-unit loads otherwise)
+    and waves left without units, against the oracle's CPU weight model (the one the decode kernels compute)."""
+    banner(f"matrix-core decode {kw}")
+    c = make_case(seed=31, **kw)
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_mfma"
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"decode {kw}")
+
+
 # ------------------------------------------------------------------------------------------------ dequantisation
 def _adversarial_q4(rows, K, seed):
     """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
