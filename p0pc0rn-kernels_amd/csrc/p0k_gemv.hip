@@ -606,7 +606,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Decode on the matrix cores with q4 weights and 3..16 rows, without staging X'. The same 128-column items as above,
+// Decode on the matrix cores with q4 weights and 3..16 rows, with no X' staging phase before the stream (the X rows
+// are copied to LDS while the first weight units are on their way). The same 128-column items as above,
 // but each of the 8 waves covers all 128 columns of one K-eighth, so each X' fragment it loads serves 8 blocks of 16
 // weight rows. Per 32-k unit a wave runs ten v_mfma_f32_16x16x32_f16, every operand in registers:
 //   * lane l loads code rows l and 64 + l of the unit (16 bytes each: one 128-bit load covers 64 rows' 1 KB) and their
@@ -624,18 +625,13 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 //   * two MFMAs against constant B operands give, for every output column, -G1 = -(1024 X_lo + 64 X_hi) and
 //     G2 = X_lo + X_hi of the unit's rows; each block's MFMA starts from -G1, so it returns sum x q directly, and
 //     y += s (sum x q) + mn G2 in registers (the fp32 weight model of the stream above).
-#ifndef P0K_MQ4_NW
-#define P0K_MQ4_NW 8
-#endif
-constexpr int MQ_KQ = P0K_MQ4_NW, MQ_NT = 64 * MQ_KQ;           // waves = K parts of an item
+// (12 or 16 waves per item, or 2 or 4 units in flight per wave, measured slower)
+constexpr int MQ_KQ = 8, MQ_NT = 64 * MQ_KQ, MQ_PF = 3;     // waves = K parts of an item; units in flight per wave
 constexpr int MQ_XP = MF_KSM * 2 + 16;                       // LDS bytes per staged X row
 constexpr int MQ_LDS = 16 * MQ_XP > MQ_KQ * 16 * 128 * 4 ? 16 * MQ_XP : MQ_KQ * 16 * 128 * 4;
-#ifndef P0K_MQ4_PF
-#define P0K_MQ4_PF 3
-#endif
 template <int XM, bool XL>
 __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
-  constexpr int MT = 16, PF = P0K_MQ4_PF;
+  constexpr int MT = 16, PF = MQ_PF;
   static_assert(!XL || XM == X_F16, "X rows are copied as they are only without a prologue");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[XL ? MQ_LDS : MQ_KQ * MT * 128 * 4];
   __shared__ uint32_t sLast;
