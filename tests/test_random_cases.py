@@ -1,0 +1,70 @@
+"""Randomised parity sweep of the gemm path on the GPU: a fixed list of cases drawn from a seeded generator over every
+weight encoding, prologue, epilogue and the offsets of the argument objects (x.ld / x.k0, y.ld / y.n0, wk0, wr0),
+with M from 1 to a few hundred rows so that every kernel (the one-row GEMV, the matrix-core decode with and without
+its K split, the load-to-LDS MFMA GEMM with its tiles and tail launch, the register-staged MFMA GEMM) gets calls of
+odd shapes. Each case is checked against the oracle with the weight model of the kernel that runs it (assert_close's
+fp16 / fp32 tolerance). The list is generated here, not stored: the same seed gives the same cases.
+"""
+import numpy as np
+import pytest
+
+import p0k
+from cases import assert_close, make_case
+
+pytestmark = pytest.mark.gpu
+
+M_CHOICES = [1, 2, 3, 5, 8, 13, 16, 17, 33, 64, 100, 129, 200, 257, 300]
+
+
+def _cases(n=96, seed=20251202):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        enc = ["q4g32a.t64", "q8g64s.t64", "f16"][rng.integers(3)]
+        xmode = ["f16", "f16", "rms", "lnmod"][rng.integers(4)]
+        epi = ["f16", "f32", "resadd", "bias", "swiglu", "onormgate", "heads"][rng.integers(7)]
+        M = int(M_CHOICES[rng.integers(len(M_CHOICES))])
+        kq = 64 if enc == "q8g64s.t64" else 32
+        # (half of them whole multiples of 256: the decode kernels split K into 4 or 8 parts of whole units)
+        K = int(kq * rng.integers(1, 1024 // kq + 1)) if rng.integers(2) else int(256 * rng.integers(1, 5))
+        kw = dict(enc=enc, xmode=xmode, epi=epi, M=M, K=K, seed=int(rng.integers(1, 1 << 20)))
+        if epi == "heads":
+            Hq, Hkv = int(rng.integers(1, 3)), int(rng.integers(1, 2))
+            kw.update(N=(Hq + 2 * Hkv) * 128, Hq=Hq, Hkv=Hkv, rope_mode=["interleaved", "half"][rng.integers(2)],
+                      row_off=int(rng.integers(0, 5)))
+        elif epi == "onormgate":
+            kw.update(N=128 * int(rng.integers(1, 4)))
+        elif epi == "swiglu":
+            kw.update(N=16 * int(rng.integers(1, 48)), act=["silu", "gelu"][rng.integers(2)], bias=bool(rng.integers(2)))
+        else:
+            kw.update(N=8 * int(rng.integers(1, 96)))
+        if epi == "resadd":
+            kw.update(gate=bool(rng.integers(2)), bias=bool(rng.integers(2)), store=bool(rng.integers(2)))
+        if epi == "bias":
+            kw.update(res=bool(rng.integers(2)))
+        # offsets: x rows / column (multiples of 4, as the reference's vec4 rows require), output column, weight
+        # column (whole groups) and first weight row (whole records)
+        if rng.integers(2):
+            kw.update(ld_pad=int(4 * rng.integers(0, 5)), k0=int(4 * rng.integers(0, 9)))
+        if epi not in ("heads", "onormgate") and rng.integers(2):
+            kw.update(n0=int(8 * rng.integers(0, 3)))
+        if rng.integers(3) == 0:
+            kw.update(wk0=kq * int(rng.integers(1, 3)))
+        if epi not in ("swiglu",) and rng.integers(4) == 0:
+            kw.update(wr0=64)
+        out.append(kw)
+    return out
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("kw", CASES, ids=[f"{i:02d}-{k['enc'][:2]}-{k['xmode']}-{k['epi']}-M{k['M']}-N{k['N']}-K{k['K']}"
+                                           for i, k in enumerate(CASES)])
+def test_random_case_matches_oracle(dev, kw):
+    c = make_case(**kw)
+    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    print(f"[p0k-test] random case {kw} kernel={kern}", flush=True)
+    got = c.run_device(dev)
+    want = c.run_oracle()
+    assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on {kern}")
