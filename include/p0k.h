@@ -39,7 +39,8 @@
 extern "C" {
 #endif
 
-#define P0K_ABI_VERSION 1
+/* 2: p0k_stream_read_probe takes the workgroup size, p0k_mfma_valu_probe the operand pattern */
+#define P0K_ABI_VERSION 2
 
 /* ---- status codes */
 enum {
