@@ -54,8 +54,9 @@ MALL = 256 << 20
 
 # HBM bytes per launch from rocprofv3 counters (profiles/k_gemv*_decode_M*.md, k_stream_read_73MB_ceiling.md): FETCH_SIZE and WRITE_SIZE in
 # KiB per dispatch, each times what the same counter reads per byte of a plain 1 GiB device copy (`--copy-calib`:
-# FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run, so the
-# figures of the last profiled build are kept here, per workload.
+# FETCH_SIZE reads half the bytes, WRITE_SIZE all of them). Counters cannot be read inside the timed run: the
+# headline's are measured by child rocprofv3 runs at the start of the bench (measure_traffic); for the other
+# workloads, and when rocprofv3 is not available, the figures of the last profiled build are kept here.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35993, 28), "decode_q4_swiglu_M4": (36250, 112), "decode_q4_swiglu_M16": (36667, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
@@ -384,6 +385,58 @@ def roofline(wl, ms):
             "frac": round(ach * 1e12 / FP16_PEAK, 4), "traffic": traffic}
 
 
+# ------------------------------------------------------------------------------------------------ live HBM traffic
+def _pmc_mean(counter, args, kernel, timeout=150):
+    """Mean per-dispatch value of one rocprofv3 counter for the kernels whose name contains `kernel`, from a child
+    `rocprofv3 --pmc <counter> -- python3 bench.py <args>` run (its own process: this one has not touched the GPU
+    yet). None when rocprofv3 is absent or the run fails."""
+    import csv
+    import glob
+    import shutil
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None
+    d = tempfile.mkdtemp(prefix="p0k_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp", P0K_BENCH_EAGER="1")
+    try:
+        r = subprocess.run([exe, "--pmc", counter, "-d", d, "-o", "run", "--output-format", "csv", "--",
+                            sys.executable, os.path.abspath(__file__)] + args, cwd="/tmp", env=env,
+                           stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, timeout=timeout)
+        if r.returncode != 0:
+            log(f"rocprofv3 --pmc {counter} failed ({r.returncode}): {r.stderr.decode(errors='replace')[-300:]}")
+            return None
+        vals = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f) as fh:
+                for row in csv.DictReader(fh):
+                    if kernel in row["Kernel_Name"] and row["Counter_Name"] == counter:
+                        vals.append(float(row["Counter_Value"]))
+        return sum(vals) / len(vals) if vals else None
+    except (OSError, subprocess.TimeoutExpired, KeyError, ValueError) as e:
+        log(f"rocprofv3 --pmc {counter}: {e}")
+        return None
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def measure_traffic():
+    """The headline kernel's HBM bytes per launch, measured in this run: FETCH_SIZE and WRITE_SIZE (KiB per dispatch,
+    one counter per rocprofv3 pass) of the decode call, each scaled by what the same counter reads per byte of a
+    plain 1 GiB device copy (`--copy-calib`) in the same way. None (and the last profiled figures are used) when any
+    pass fails."""
+    big = ["--only", "decode1", "--no-cpu", "--no-traffic", "--steps", "10", "--warmup", "2"]
+    fetch = _pmc_mean("FETCH_SIZE", big, "k_gemv")
+    write = _pmc_mean("WRITE_SIZE", big, "k_gemv")
+    cf = _pmc_mean("FETCH_SIZE", ["--copy-calib"], "copyBuffer") if fetch is not None else None
+    cw = _pmc_mean("WRITE_SIZE", ["--copy-calib"], "copyBuffer") if write is not None else None
+    if None in (fetch, write, cf, cw) or cf <= 0 or cw <= 0:
+        return None
+    ff, wf = (1 << 30) / (cf * 1024), (1 << 30) / (cw * 1024)
+    return {"bytes": int(fetch * 1024 * ff + write * 1024 * wf), "fetch_kib": round(fetch, 1), "write_kib": round(write, 1),
+            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 def cpu_baseline(config, rows, target_s=0.0):
     """Run the JavaScript CPU restatement in Node: one call over `rows` rows of M, repeated for about target_s seconds
@@ -522,6 +575,7 @@ def main():
     ap.add_argument("--mfma-ceiling", action="store_true")
     ap.add_argument("--hbm-ceiling", action="store_true")
     ap.add_argument("--library-gemm", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the live counter runs of the headline's traffic")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (the gemm path has no multi-GPU mode here); run with --gpus 1",
@@ -534,6 +588,10 @@ def main():
         library_gemm()
         return
     names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
+    live_traffic = None
+    if not a.no_traffic and "decode1" in names and not (a.mfma_ceiling or a.hbm_ceiling):
+        live_traffic = measure_traffic()           # child processes, before this one touches the GPU
+        log(f"headline traffic from counters in this run: {live_traffic}")
     dev = p0k.Device(0)
     if a.mfma_ceiling:
         mfma_ceiling(dev)
@@ -606,7 +664,11 @@ def main():
         "dtype": "q4 weights (u4 codes -> fp16), fp16 activations, fp32 accumulate", "data": "synthetic (seeded PCG64)",
         "config": {"workload": head["name"], "M": head["M"], "N": 28672, "K": 4096, "enc": "q4g32a.t64", "epi": "swiglu",
                    "weight_copies_rotated": head.get("weight_copies")},
-        "roofline": head["roofline"],
+        "roofline": (dict(head["roofline"], traffic=live_traffic["bytes"], traffic_source="rocprofv3 FETCH_SIZE + "
+                          "WRITE_SIZE of the headline kernel in this run, scaled by a 1 GiB copy's counts")
+                     if live_traffic and head is results.get("decode1") else
+                     dict(head["roofline"], traffic_source="counters of the last profiled build (TRAFFIC_KIB)")),
+        "traffic_counters": live_traffic if head is results.get("decode1") else None,
         "cpu_baseline": ({"value": round(head["algo_bytes"] / (cpu["ms_per_call"] * 1e6), 3), "unit": "GB/s",
                           "cores": cores, "kind": "port",
                           "sample": f"{cpu['sample']}; oracle/cpu_ref.mjs on Node {cpu['node']}, one thread of "
