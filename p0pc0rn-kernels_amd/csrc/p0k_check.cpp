@@ -56,6 +56,7 @@ Tuning tuning_from_env(unsigned cus) {
   if (const char *ov = getenv("P0K_GEMV_MF")) t.gemv_mf = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_GEMV_MQ4")) t.gemv_mq4 = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_GEMV_SLICES")) t.gemv_slices = (unsigned)std::max(0, atoi(ov));
+  if (const char *ov = getenv("P0K_GEMV_MX")) t.gemv_mx = (unsigned)std::max(0, atoi(ov));
   if (const char *ov = getenv("P0K_MFMA_KERNEL")) t.mfma_reg = strcmp(ov, "reg") == 0;
   if (const char *ov = getenv("P0K_MFMA_TILE")) {
     unsigned tm = 0, tn = 0;
@@ -248,6 +249,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M)
   int kernel = K_MFMA;
   unsigned S = 0, KS = 0;
+  bool mx = false;
   if (M <= (uint32_t)GEMV_MAX_M && (xm == P0K_X_F16 || xf32) && M > 0) {
     // the GEMV reads q8 in whole 64-k records and f16 rows with 16-byte loads only
     // and addresses the tensor with 32-bit offsets
@@ -259,18 +261,23 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // f16 its per-lane loads read 16 of every 64 bytes per load: q8 2.8 vs 3.6 TB/s, f16 1.4 vs 3.7)
       bool mf = M >= 3 || we != P0K_ENC_Q4G32A_T64;
       if (tune.gemv_mf >= 0) mf = mf && tune.gemv_mf != 0;   // tuning: the VALU stream for M > 1
-      gemv_split(p, we, tune.cus, mf, &S, &KS);
+      // q4 with 2..4 rows (P0K_GEMV_MX): the one-row stream with its per-unit sums on the matrix cores (4x4x4 blocks,
+      // each lane's own weight row as a B column): 14.6-15.2 us at M = 2..4 against 15.3 (dot products) and 16.1-16.3
+      // (k_gemv_mq4); with 8 or 16 rows it is slower than k_gemv_mq4 (18.3 / 28.0 vs 16.8 / 17.9 us)
+      mx = we == P0K_ENC_Q4G32A_T64 && M >= 2 && M <= tune.gemv_mx;
+      if (mx) mf = false;
+      gemv_split(p, we, tune.cus, mf, mx, &S, &KS);
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
       if (tune.gemv_slices) {
         unsigned s2 = tune.gemv_slices, quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
-        if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, mf)) { S = s2; KS = K / s2; }
+        if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
     }
   }
   if (out) *out = p;
   if (plan) {
-    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128;
+    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128; plan->mx = mx;
     // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
     if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes) && !tune.mfma_reg) kernel = plan->kernel = K_MFMA_DMA;
     if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, tune.cus, &plan->bm, &plan->bn);

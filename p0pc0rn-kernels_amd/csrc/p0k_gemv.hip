@@ -53,6 +53,22 @@ struct Unit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
 template <int MT>
 constexpr int ks_max() { return (GV_LDS * 8 / (MT * 18)) & ~1023; }
 
+// q4 with 4, 8 or 16 rows (MX): the unit's dot products run on the matrix cores as v_mfma_f32_4x4x4_16b_f16 with the
+// lane's own weight row as the B column (below); X' rows padded by 16 bytes, and a larger LDS budget so that K = 4096
+// (8192 at 4 rows) needs no split
+#ifndef P0K_MX_PF
+#define P0K_MX_PF 4
+#endif
+#ifndef P0K_MX_PX
+#define P0K_MX_PX 4
+#endif
+template <int WE, int MT>
+constexpr bool gv_mx() { return WE == W_Q4 && MT >= 4; }
+template <int MT>
+constexpr int mx_ksm() { return MT == 4 ? 8192 : 4096; }
+template <int MT>
+constexpr int mx_lds() { return MT * (mx_ksm<MT>() + 8) * 2 + mx_ksm<MT>() / 32 * MT * 4; }
+
 // One call's tile without a K split, for the element-wise epilogues (f16, f32, bias, resadd, swiglu): one thread per
 // output element sums the element's K-quarters (in quarter order, as finish() does) and applies the epilogue, so the
 // tile needs no summing pass of its own and every thread has a few instructions of work (the 16-byte-store epilogue
@@ -153,15 +169,19 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
 
 template <int WE, int XM, int MT>
 __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
-  constexpr int UK = Unit<WE>::UK, PF = Unit<WE>::PF, KSM = ks_max<MT>(), NGM = KSM / UK;
-  static_assert(GV_KSUB * MT * 128 * 4 <= GV_LDS, "partials must fit the staging buffer");
+  constexpr bool MX = gv_mx<WE, MT>();
+  constexpr int UK = Unit<WE>::UK, PF = MX ? P0K_MX_PF : Unit<WE>::PF, KSM = MX ? mx_ksm<MT>() : ks_max<MT>(), NGM = KSM / UK;
+  constexpr int XSTR = MX ? KSM + 8 : KSM;                     // halves per staged X' row
+  constexpr int LDSB = MX ? mx_lds<MT>() : GV_LDS;
+  static_assert(GV_KSUB * MT * 128 * 4 <= LDSB, "partials must fit the staging buffer");
   // one or two rows: the partials get their own 2-4 KB, so the waves write them as they finish their streams without
   // waiting for each other; more rows: the partials reuse the X' buffer after a barrier
   constexpr bool SEP = MT <= 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[GV_LDS + (SEP ? GV_KSUB * MT * 128 * 4 : 0)];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LDSB + (SEP ? GV_KSUB * MT * 128 * 4 : 0)];
   __shared__ uint32_t sLast;
-  f16 *sX = (f16 *)smem;                                       // [MT][KSM] X', pair order of the encoding
-  f32x2 *sG = (f32x2 *)(smem + MT * KSM * 2);                  // [MT][KSM / UK] (Xlo, Xhi) per unit
+  f16 *sX = (f16 *)smem;                                       // [MT][XSTR] X', pair order of the encoding
+  f32x2 *sG = (f32x2 *)(smem + MT * XSTR * 2);                 // [MT][KSM / UK] (Xlo, Xhi) per unit
+  float *sGx = (float *)(smem + MT * XSTR * 2);                // MX: [KSM / UK][MT] X = Xlo + Xhi per unit and row
   float *sR = (float *)(smem + (SEP ? GV_LDS : 0));            // after the stream: partials
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -208,7 +228,43 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 
   auto compute = [&](const Unit<WE> &u, uint32_t unit) {
     const f16 *xs = sX + unit * UK;
-    if constexpr (WE == W_Q4) {
+    if constexpr (MX) {
+      // 16 blocks of 4 x 4 x 4: lane l supplies B column (weight row of the lane) of block l / 4 and A row l % 4 (X'
+      // row 4 g + l % 4, the same 4 rows for every block), and receives D[m = 4 g + r][its weight row], r = 0..3. B
+      // holds q and 16 q (the magic-biased halves minus 1024, exact), X' at the high-nibble positions is staged as
+      // x / 16, so one chain over the unit's 8 steps of 4 k returns sum x q; then y += s (sum x q) + mn X in fp32, as
+      // in the dot-product form below. (Started from -G1 on the biased codes instead, the chain's partial sums sit
+      // near 1024 X and its eight fp32 roundings there cost more than the fp32 sums of the other decode kernels.)
+      const uint32_t wd[4] = {u.code.x, u.code.y, u.code.z, u.code.w};
+      const f16x2 k1024 = {(f16)1024.0f, (f16)1024.0f};
+      uint32_t h[16];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t w8 = wd[i] >> 8;
+        h[4 * i + 0] = as_u(as_h2((wd[i] & mlo) | mag) - k1024);
+        h[4 * i + 1] = as_u(as_h2((wd[i] & mhi) | mag) - k1024);
+        h[4 * i + 2] = as_u(as_h2((w8 & mlo) | mag) - k1024);
+        h[4 * i + 3] = as_u(as_h2((w8 & mhi) | mag) - k1024);
+      }
+      const f16x2 sm2 = as_h2(u.sm);
+      const float s = (float)sm2.x, mn = (float)sm2.y;
+#pragma unroll
+      for (int g = 0; g < MT / 4; g++) {
+        const u32x4 *x4 = (const u32x4 *)(xs + (4 * g + (lane & 3)) * XSTR);
+        const f32x4 g2 = *(const f32x4 *)(sGx + unit * MT + 4 * g);
+        f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 xv = x4[i];
+          d = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4, (u32x2){xv.x, xv.y}),
+                                                 __builtin_bit_cast(f16x4, (u32x2){h[4 * i + 0], h[4 * i + 1]}), d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4, (u32x2){xv.z, xv.w}),
+                                                 __builtin_bit_cast(f16x4, (u32x2){h[4 * i + 2], h[4 * i + 3]}), d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[4 * g + r] = fmaf(s, d[r], fmaf(mn, g2[r], acc[4 * g + r]));
+      }
+    } else if constexpr (WE == W_Q4) {
       const uint32_t wd[4] = {u.code.x, u.code.y, u.code.z, u.code.w};
       uint32_t h[16];                                           // per word: (q0,q4) (16q1,16q5) (q2,q6) (16q3,16q7)
 #pragma unroll
@@ -282,13 +338,17 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
     }
   };
 
-  // This thread's first chunk of X is loaded before the ring: loads return in issue order (one vmcnt counter per
-  // wave), so an X load issued after the ring would wait for the ring's first units and hold the staging back.
+  // This thread's first chunks of X (one; four with the matrix-core form, whose 4 rows take four) are loaded before
+  // the ring: loads return in issue order (one vmcnt counter per wave), so an X load issued after the ring would wait
+  // for the ring's first units and hold the staging back.
+  constexpr int PX = MX ? P0K_MX_PX : 1;
   const uint32_t nb = KS / 8, nx = MT * nb;
-  u32x4 xv0 = (u32x4){0u, 0u, 0u, 0u};
-  {
-    const uint32_t m = (uint32_t)tid / nb;
-    if ((uint32_t)tid < nx && m < p.M) xv0 = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * ((uint32_t)tid - m * nb));
+  u32x4 xv0[PX];
+#pragma unroll
+  for (int i = 0; i < PX; i++) {
+    const uint32_t t = (uint32_t)tid + (uint32_t)(i * GV_NT), m = t / nb;
+    xv0[i] = (u32x4){0u, 0u, 0u, 0u};
+    if (t < nx && m < p.M) xv0[i] = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * (t - m * nb));
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -304,12 +364,9 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   // X' of the slice -> LDS in the pair order of the encoding, and per unit the X' sums over the low (even pair slot)
   // and high (odd pair slot) positions: a unit's UK / 8 chunks sit in as many adjacent lanes (nx and the thread count
   // are multiples of UK / 8, so such a lane group is active or idle as a whole), which sum across by shuffles
-  for (uint32_t t = tid; t < nx; t += GV_NT) {
+  auto stage = [&](uint32_t t, u32x4 v) __attribute__((always_inline)) {
     const uint32_t m = t / nb, kq = t - m * nb;
-    u32x4 v = xv0;
-    if (t != (uint32_t)tid) v = m < p.M ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * kq) : (u32x4){0u, 0u, 0u, 0u};
     v = xperm<WE>(v);
-    *(u32x4 *)(sX + m * KSM + 8 * kq) = v;
     if constexpr (WE != W_F16) {
       const f16x2 a = as_h2(v.x), b = as_h2(v.y), c = as_h2(v.z), d = as_h2(v.w);
       float lo = ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
@@ -319,8 +376,25 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
         lo += __shfl_xor(lo, o);
         hi += __shfl_xor(hi, o);
       }
-      if (kq % (UK / 8) == 0) sG[m * NGM + kq / (UK / 8)] = (f32x2){lo, hi};
+      if constexpr (MX) {
+        if (kq % (UK / 8) == 0) sGx[(kq / (UK / 8)) * MT + m] = lo + hi;
+        const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+        v.y = as_u(as_h2(v.y) * r16);
+        v.w = as_u(as_h2(v.w) * r16);
+      } else if (kq % (UK / 8) == 0) {
+        sG[m * NGM + kq / (UK / 8)] = (f32x2){lo, hi};
+      }
     }
+    *(u32x4 *)(sX + m * XSTR + 8 * kq) = v;
+  };
+#pragma unroll
+  for (int i = 0; i < PX; i++) {
+    const uint32_t t = (uint32_t)tid + (uint32_t)(i * GV_NT);
+    if (t < nx) stage(t, xv0[i]);
+  }
+  for (uint32_t t = (uint32_t)tid + (uint32_t)(PX * GV_NT); t < nx; t += GV_NT) {
+    const uint32_t m = t / nb;
+    stage(t, m < p.M ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + 8 * (t - m * nb)) : (u32x4){0u, 0u, 0u, 0u});
   }
   __syncthreads();
 
@@ -778,18 +852,30 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   else finish<MT, MQ_KQ, MQ_NT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
-static uint32_t ks_max_of(uint32_t M, bool mf) {
-  if (mf) return MF_KSM;
-  return M <= 1 ? ks_max<1>() : M <= 2 ? ks_max<2>() : M <= 4 ? ks_max<4>() : M <= 8 ? ks_max<8>() : ks_max<16>();
+// the row tile of the stream kernel: q4 with mx takes the matrix-core form (4 rows) at M = 2 too
+static uint32_t stream_mt(uint32_t M, int we, bool mx) {
+  return M <= 1 ? 1u : (M <= 2 && !(we == W_Q4 && mx)) ? 2u : M <= 4 ? 4u : M <= 8 ? 8u : 16u;
 }
-unsigned gemv_ks_max(unsigned M, bool mf) { return ks_max_of(M, mf); }
+template <int MT>
+static uint32_t stream_ksm(int we) { return we == W_Q4 && gv_mx<W_Q4, MT>() ? (uint32_t)mx_ksm<MT>() : (uint32_t)ks_max<MT>(); }
+static uint32_t ks_max_of(uint32_t M, int we, bool mf, bool mx) {
+  if (mf) return MF_KSM;
+  switch (stream_mt(M, we, mx)) {
+  case 1: return stream_ksm<1>(we);
+  case 2: return stream_ksm<2>(we);
+  case 4: return stream_ksm<4>(we);
+  case 8: return stream_ksm<8>(we);
+  }
+  return stream_ksm<16>(we);
+}
+unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx) { return ks_max_of(M, we, mf, mx); }
 
 // Slices per tile: the fewest that fill the GPU with items (about one per CU) and keep each slice's X' inside the LDS
 // budget, with a whole number of units per K-quarter.
-void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S_out, unsigned *KS_out) {
+void gemv_split(const Params &p, int we, unsigned cus, bool mf, bool mx, unsigned *S_out, unsigned *KS_out) {
   const uint32_t tiles = (p.N + 127) / 128;
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;     // k per "one unit in each K-quarter"
-  const uint32_t ksm = ks_max_of(p.M, mf);
+  const uint32_t ksm = ks_max_of(p.M, we, mf, mx);
   uint32_t S = 1;
   while ((tiles * S < cus * 7u / 8u || p.K / S > ksm) && p.K % (2u * S * quant) == 0) S *= 2u;
   if (p.K % (S * quant) != 0 || p.K / S > ksm) S = 0;             // caller falls back to the MFMA kernel
@@ -799,14 +885,14 @@ void gemv_split(const Params &p, int we, unsigned cus, bool mf, unsigned *S_out,
 
 template <int WE, int XM, int MT>
 static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
-  if (KS > (uint32_t)ks_max<MT>()) return hipErrorInvalidValue;
+  if (KS > (uint32_t)(gv_mx<WE, MT>() ? mx_ksm<MT>() : ks_max<MT>())) return hipErrorInvalidValue;
   dim3 grid(((p.N + 127) / 128) * S);
   hipLaunchKernelGGL((k_gemv<WE, XM, MT>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
   return hipGetLastError();
 }
 template <int WE, int XM>
 static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s, bool mf,
-                          bool mq4) {
+                          bool mq4, bool mx) {
   if (mf) {
     if (KS > (uint32_t)MF_KSM) return hipErrorInvalidValue;
     dim3 grid(((p.N + 127) / 128) * S);
@@ -818,31 +904,33 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
     hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
   }
-  if (p.M <= 1) return launch3<WE, XM, 1>(p, part, cnt, S, KS, s);
-  if (p.M <= 2) return launch3<WE, XM, 2>(p, part, cnt, S, KS, s);
-  if (p.M <= 4) return launch3<WE, XM, 4>(p, part, cnt, S, KS, s);
-  if (p.M <= 8) return launch3<WE, XM, 8>(p, part, cnt, S, KS, s);
+  switch (stream_mt(p.M, WE, mx)) {
+  case 1: return launch3<WE, XM, 1>(p, part, cnt, S, KS, s);
+  case 2: return launch3<WE, XM, 2>(p, part, cnt, S, KS, s);
+  case 4: return launch3<WE, XM, 4>(p, part, cnt, S, KS, s);
+  case 8: return launch3<WE, XM, 8>(p, part, cnt, S, KS, s);
+  }
   return launch3<WE, XM, 16>(p, part, cnt, S, KS, s);
 }
 template <int WE>
 static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s,
-                          bool mf, bool mq4) {
+                          bool mf, bool mq4, bool mx) {
   switch (xm) {
-  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf, mq4);
-  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf, mq4);
-  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf, mq4);
+  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf, mq4, mx);
+  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf, mq4, mx);
+  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf, mq4, mx);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
-                       hipStream_t s, bool mf, bool mq4) {
+                       hipStream_t s, bool mf, bool mq4, bool mx) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
   switch (we) {
-  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4);
-  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4);
-  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf, mq4);
+  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
+  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
+  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
   }
   return hipErrorInvalidValue;
 }

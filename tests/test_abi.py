@@ -131,8 +131,9 @@ def test_kernel_choice():
     assert p0k.select_tile(host_args(make_case(M=1, enc="q4g32a.t64")))["kernel"] == "gemv"
     assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv_mfma"              # f16 / q8 rows: matrix cores
     assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
-    assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, two rows: VALU
-    assert p0k.select_tile(host_args(make_case(M=3, enc="q4g32a.t64")))["kernel"] == "gemv_mfma"
+    assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, 2..4 rows: stream
+    assert p0k.select_tile(host_args(make_case(M=4, enc="q4g32a.t64")))["kernel"] == "gemv"
+    assert p0k.select_tile(host_args(make_case(M=5, enc="q4g32a.t64")))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=17)))["kernel"] == "mfma_dma"          # fp16 rows, K % 64 == 0
     assert p0k.select_tile(host_args(make_case(M=17, K=96)))["kernel"] == "mfma"         # K % 64 != 0
@@ -200,6 +201,19 @@ def test_tuning_switches_read_per_call_without_a_context(monkeypatch):
     monkeypatch.delenv("P0K_MFMA_KERNEL")
     monkeypatch.delenv("P0K_MFMA_TILE")
     assert p0k.select_tile(a) == base
+
+
+def test_decode_row_routing_switch(monkeypatch):
+    """P0K_GEMV_MX=n sends q4 decode calls with 2..n rows to the stream kernel's matrix-core form (kernel "gemv");
+    the default is 4, beyond it the q4 matrix-core decode (k_gemv_mq4, "gemv_mfma") takes the call."""
+    q4 = lambda M: p0k.select_tile(host_args(make_case(M=M, enc="q4g32a.t64", N=256, K=512)))["kernel"]   # noqa: E731
+    assert [q4(M) for M in (1, 2, 3, 4, 5, 16)] == ["gemv"] * 4 + ["gemv_mfma"] * 2
+    monkeypatch.setenv("P0K_GEMV_MX", "0")
+    assert [q4(M) for M in (1, 2, 3, 4)] == ["gemv", "gemv", "gemv_mfma", "gemv_mfma"]
+    monkeypatch.setenv("P0K_GEMV_MX", "16")
+    assert [q4(M) for M in (5, 8, 16)] == ["gemv"] * 3
+    # q8 / f16 weights never take it
+    assert p0k.select_tile(host_args(make_case(M=4, enc="q8g64s.t64", N=256, K=512)))["kernel"] == "gemv_mfma"
 
 
 def test_null_context_calls_are_refused():

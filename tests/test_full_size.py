@@ -52,16 +52,19 @@ def oracle_rows(case, ranges, weights):
     return want
 
 
-@pytest.mark.parametrize("M,staged", [(1, False), (4, False), (16, False), (16, True)])
-def test_decode_q4_swiglu_full(dev, M, staged, monkeypatch):
-    """q4 N = 14336 (gate | up: 28672 weight rows), K = 4096, SwiGLU; every output row. staged: the
-    matrix-core decode with X' staged in LDS before the stream (P0K_GEMV_MQ4=0) instead of k_gemv_mq4."""
-    if staged:
+@pytest.mark.parametrize("M,path", [(1, "stream"), (2, "mx"), (4, "mx"), (8, "mx"), (16, "mx"), (4, "mq4"), (16, "mq4"),
+                                    (16, "staged")])
+def test_decode_q4_swiglu_full(dev, M, path, monkeypatch):
+    """q4 N = 14336 (gate | up: 28672 weight rows), K = 4096, SwiGLU; every output row. mx: the stream
+    kernel with its 4x4x4 matrix-core dot products (P0K_GEMV_MX=16); mq4: k_gemv_mq4 (P0K_GEMV_MX=0); staged: the
+    matrix-core decode with X' staged in LDS before the stream (P0K_GEMV_MX=0 P0K_GEMV_MQ4=0)."""
+    monkeypatch.setenv("P0K_GEMV_MX", "16" if path == "mx" else "0")
+    if path == "staged":
         monkeypatch.setenv("P0K_GEMV_MQ4", "0")
-    banner(f"full-size decode M={M} staged={staged}")
+    banner(f"full-size decode M={M} path={path}")
     c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=28672, K=4096, seed=101, wscale=0.02)
     t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
-    assert t["kernel"] == ("gemv" if M == 1 else "gemv_mfma")
+    assert t["kernel"] == ("gemv" if path in ("stream", "mx") else "gemv_mfma")
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"decode M={M}")
 

@@ -103,7 +103,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    assert kern == ("gemv" if M <= 2 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
+    assert kern == ("gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
@@ -128,14 +128,18 @@ DECODE_OFFSET_CASES = [
 ]
 
 
+@pytest.mark.parametrize("path", ["mq4", "mx"])
 @pytest.mark.parametrize("kw", DECODE_OFFSET_CASES, ids=lambda k: f"M{k['M']}-K{k['K']}-pad{k.get('ld_pad', 0)}-k0{k.get('k0', 0)}")
-def test_matrix_core_decode_offsets(dev, kw):
-    """q4 decode with 3..16 rows (k_gemv_mq4): X row pitch / column offset, weight column and row offsets, output
-    column offset; both ways the kernel gets its A fragments (LDS copy of aligned X rows, per-unit loads otherwise)
-    and waves left without units, against the oracle's CPU weight model (the one the decode kernels compute)."""
-    banner(f"matrix-core decode {kw}")
+def test_matrix_core_decode_offsets(dev, kw, path, monkeypatch):
+    """q4 decode with 3..16 rows: X row pitch / column offset, weight column and row offsets, output column offset;
+    mq4 (k_gemv_mq4, P0K_GEMV_MX=0): both ways the kernel gets its A fragments (LDS copy of aligned X rows, per-unit
+    loads otherwise) and waves left without units; mx (the stream kernel's 4x4x4 matrix-core form for 4, 8 and 16
+    rows, P0K_GEMV_MX=16): the same calls. Against the oracle's CPU weight model (the one the decode kernels
+    compute)."""
+    monkeypatch.setenv("P0K_GEMV_MX", "0" if path == "mq4" else "16")
+    banner(f"matrix-core decode {path} {kw}")
     c = make_case(seed=31, **kw)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_mfma"
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv_mfma" if path == "mq4" else "gemv")
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"decode {kw}")
 
@@ -160,14 +164,19 @@ def _adversarial_q8(rows, K, seed):
 
 
 @pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
-@pytest.mark.parametrize("path", ["gemv", "gemv_mfma", "gemv_mfma_staged", "mfma"])
+@pytest.mark.parametrize("path", ["gemv", "gemv_mx2", "gemv_mx8", "gemv_mx16", "gemv_mfma", "gemv_mfma_staged", "mfma"])
 def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
     to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream;
-    P0K_GEMV_MQ4=0 the q4 matrix-core decode with X' staged in LDS.)"""
+    P0K_GEMV_MX=16 the stream kernel's 4x4x4 matrix-core form for q4 with 2..16 rows; P0K_GEMV_MQ4=0 the q4
+    matrix-core decode with X' staged in LDS.)"""
+    if path.startswith("gemv_mx") and not enc.startswith("q4"):
+        pytest.skip("the stream kernel's matrix-core form is q4 only")
     if path == "gemv":
         monkeypatch.setenv("P0K_GEMV_MF", "0")
+    if path.startswith("gemv_mx"):
+        monkeypatch.setenv("P0K_GEMV_MX", "16")
     if path == "gemv_mfma_staged":
         monkeypatch.setenv("P0K_GEMV_MQ4", "0")
     rows, K = 128, 256
@@ -175,7 +184,7 @@ def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
     dw = dev.upload(wb)
     try:
-        M = {"gemv": 1, "gemv_mfma": 16, "gemv_mfma_staged": 16, "mfma": K}[path]
+        M = {"gemv": 1, "gemv_mx2": 2, "gemv_mx8": 8, "gemv_mx16": 16, "gemv_mfma": 16, "gemv_mfma_staged": 16, "mfma": K}[path]
         got = np.zeros((K, rows), np.uint16)
         for k0 in range(0, K, M):
             X = np.zeros((M, K), np.float32)

@@ -66,7 +66,7 @@ def test_host_helpers_and_errors(tmp_path):
     assert e["rms_stats"]["message"].startswith("gemm: missing binding ST")           # :313
     assert "Ci % 32" in e["conv3_ci"]["message"]
     assert not any(e[k]["gpuError"] for k in ("encoding", "kmul32", "tile", "rms_stats", "conv3_ci"))
-    assert e["ok"] is None and e["plan"]["kernel"] == "gemv_mfma"
+    assert e["ok"] is None and e["plan"]["kernel"] == "gemv"                           # q4, M = 4: the stream kernel
     assert e["bytes"] == [128 // 64 * 256 // 32 * 1280, 128 // 64 * 256 // 64 * 4224, 128 * 256 * 2]
 
 
