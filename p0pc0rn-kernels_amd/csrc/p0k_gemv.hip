@@ -428,7 +428,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Decode on the matrix cores (3 <= M <= 16 for q4, M <= 16 for q8 / f16). With several rows of X the per-row dot products of the stream above
+// Decode on the matrix cores (q4 with 3..16 rows when k_gemv_mq4 is switched off, M <= 16 for q8 / f16). With several rows of X the per-row dot products of the stream above
 // multiply its VALU work; here the same items, waves and ring feed v_mfma_f32_16x16x32_f16 instead. Per 32-k step
 // (q4, f16; 64-k for q8) a wave runs one MFMA per block of 16 of its 64 weight rows: A = X' (16 rows, zero past M),
 // B = the block's weights. Lane l supplies, for block i, weight row 16 i + l%16 and the 8 k at 8 (l/16) of the step
@@ -680,7 +680,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Decode on the matrix cores with q4 weights and 3..16 rows, with no X' staging phase before the stream (the X rows
+// Decode on the matrix cores with q4 weights and 5..16 rows (3..16 with the stream kernel's matrix-core form switched
+// off), with no X' staging phase before the stream (the X rows
 // are copied to LDS while the first weight units are on their way). The same 128-column items as above,
 // but each of the 8 waves covers all 128 columns of one K-eighth, so each X' fragment it loads serves 8 blocks of 16
 // weight rows. Per 32-k unit a wave runs ten v_mfma_f32_16x16x32_f16, every operand in registers:
