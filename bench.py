@@ -456,6 +456,7 @@ def cpu_baseline(config, rows, target_s=0.0):
     return json.loads(out.stdout.strip().splitlines()[-1])
 
 
+HBM_SECONDARY_CALLS = 1000   # timed calls of each memory-bound workload other than the headline (at least)
 CPU_HEADLINE_S = 10.0   # seconds of CPU work timed for the headline workload (whole calls, repeated)
 CPU_SAMPLE = {   # workload -> (cpu_ref config, rows of M timed)
     "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 4), "decode_q4_swiglu_M16": ("decode", 8),
@@ -606,7 +607,9 @@ def main():
     results = {}
     for n in names:
         wl = BUILDERS[n](dev)
-        steps = a.steps if wl.bound == "hbm" else max(10, a.steps // 10)
+        # the headline runs exactly --steps calls; the other memory-bound lines (10-20 us per call) at least
+        # HBM_SECONDARY_CALLS, so that one slow graph replay of a short burst does not decide their mean
+        steps = (a.steps if n == "decode1" else max(a.steps, HBM_SECONDARY_CALLS)) if wl.bound == "hbm" else max(10, a.steps // 10)
         ms, wall_ms, count, dist = time_workload(dev, wl, steps, a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10))
         rf = roofline(wl, ms)
         res = {"name": wl.name, "desc": wl.desc, "M": wl.M, "ms_per_call": round(ms, 5), "calls": count,
