@@ -144,6 +144,20 @@ def test_matrix_core_decode_offsets(dev, kw, path, monkeypatch):
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"decode {kw}")
 
 
+@pytest.mark.parametrize("M,K,slices", [(2, 8192, 1), (4, 8192, 1), (4, 8192, 0), (3, 16384, 0), (4, 12288, 0)])
+def test_matrix_core_stream_long_k(dev, M, K, slices, monkeypatch):
+    """q4 decode with 2..4 rows on the stream kernel's matrix-core form at long K: one slice of 8192 (its largest
+    X' staging, P0K_GEMV_SLICES=1) and K split over slices that meet through the workspace (the planner's choice for
+    these 4 column tiles), against the oracle's CPU weight model."""
+    if slices:
+        monkeypatch.setenv("P0K_GEMV_SLICES", str(slices))
+    banner(f"matrix-core stream M={M} K={K} slices={slices}")
+    c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=512, K=K, seed=41)
+    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"stream M={M} K={K}")
+
+
 # ------------------------------------------------------------------------------------------------ dequantisation
 def _adversarial_q4(rows, K, seed):
     """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
