@@ -30,6 +30,11 @@ vendor library's plain fp16 GEMM at the configs' shapes for scale.
 
 the streaming-read ceiling of the headline's 73.4 MB over several launch shapes (p0k_stream_read_probe).
 
+    python bench.py --lds-ceiling
+
+the LDS read bandwidth of one CU (bytes per shader clock) and the clock the part held, with 4, 8 and 16 waves
+(p0k_lds_read_probe).
+
     python bench.py --copy-calib
 
 runs only a plain device-to-device copy of 1 GiB, 5 times (torch's copy kernel): the reference workload for scaling the
@@ -492,6 +497,31 @@ def mfma_probe_rate(dev, sink, v, wps, iters, rnd):
     return ms, round(flop / ms / 1e9, 1), round(flop / ms / 1e9 / (FP16_PEAK / 1e12), 4)
 
 
+def lds_ceiling(dev, iters=4096):
+    """`--lds-ceiling`: LDS read bandwidth of one CU with 4, 8 and 16 waves issuing conflict-free 16-byte reads
+    (p0k_lds_read_probe, one workgroup per CU, all CUs). Each wave records the shader clock and the 100 MHz reference
+    clock around its loop; per CU the loop runs from its first wave's start to its last wave's end, so the line gives
+    bytes per shader clock of a CU and the clock the part held, averaged over the CUs of the second launch."""
+    cus = dev.cus()
+    clk = dev.buffer(32 * 16 * cus)
+    rows = []
+    for waves in (4, 8, 16):
+        for _ in range(2):                                   # the first launch warms up, the second is read
+            dev.lds_read_probe(waves, iters, clk)
+            dev.done()
+        t = dev.read(clk, np.uint64, 4 * waves * cus).reshape(cus, waves, 4).astype(np.float64)
+        cyc = t[:, :, 1].max(axis=1) - t[:, :, 0].min(axis=1)
+        ref = (t[:, :, 3].max(axis=1) - t[:, :, 2].min(axis=1)) / 100e6
+        nbytes = waves * 64 * 16 * 16.0 * iters
+        rows.append({"waves": waves, "bytes_per_clock_per_cu": round(float(np.mean(nbytes / cyc)), 1),
+                     "gb_s_per_cu": round(float(np.mean(nbytes / ref)) / 1e9, 1),
+                     "clock_ghz": round(float(np.mean(cyc / ref)) / 1e9, 3)})
+        log(f"lds ceiling, {waves} waves: {rows[-1]}")
+    dev.free(clk)
+    print(json.dumps({"lds_read_ceiling": rows, "what": "16-byte conflict-free LDS reads per lane, one workgroup per "
+                      "CU, all CUs (p0k_lds_read_probe)", "iters": iters}), flush=True)
+
+
 def mfma_ceiling(dev):
     """`--mfma-ceiling`: FLOP rate of 8 independent 32x32x16 fp16 MFMAs per iteration with V packed-fp16 FMAs per
     MFMA, one and two waves per SIMD (p0k_mfma_valu_probe), timed with events on the library's stream; first with
@@ -575,6 +605,7 @@ def main():
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--mfma-ceiling", action="store_true")
     ap.add_argument("--hbm-ceiling", action="store_true")
+    ap.add_argument("--lds-ceiling", action="store_true")
     ap.add_argument("--library-gemm", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the live counter runs of the headline's traffic")
     a = ap.parse_args()
@@ -590,7 +621,7 @@ def main():
         return
     names = [n for n in (a.only.split(",") if a.only else BUILDERS)]
     live_traffic = None
-    if not a.no_traffic and "decode1" in names and not (a.mfma_ceiling or a.hbm_ceiling):
+    if not a.no_traffic and "decode1" in names and not (a.mfma_ceiling or a.hbm_ceiling or a.lds_ceiling):
         live_traffic = measure_traffic()           # child processes, before this one touches the GPU
         log(f"headline traffic from counters in this run: {live_traffic}")
     dev = p0k.Device(0)
@@ -600,6 +631,10 @@ def main():
         return
     if a.hbm_ceiling:
         hbm_ceiling_sweep(dev, a.steps, a.warmup)
+        dev.close()
+        return
+    if a.lds_ceiling:
+        lds_ceiling(dev)
         dev.close()
         return
     info = dev.info()

@@ -39,8 +39,8 @@
 extern "C" {
 #endif
 
-/* 2: p0k_stream_read_probe takes the workgroup size, p0k_mfma_valu_probe the operand pattern */
-#define P0K_ABI_VERSION 2
+/* 2: p0k_stream_read_probe takes the workgroup size, p0k_mfma_valu_probe the operand pattern; 3: p0k_lds_read_probe */
+#define P0K_ABI_VERSION 3
 
 /* ---- status codes */
 enum {
@@ -239,6 +239,12 @@ int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_
  *      rate alone); 1: pseudo-random fp16 operands, distinct per lane and accumulator (the rate the matrix cores hold
  *      on real data, whose power draw sets the clock). sink: a live 4-byte buffer the kernel may write. */
 int p0k_mfma_valu_probe(p0k_ctx *ctx, int valu_per_mfma, int waves_per_simd, int iters, int random_operands, float *sink);
+/*      the LDS read ceiling (no counterpart in the reference): one workgroup of `waves` (4, 8 or 16) waves per CU, each
+ *      lane `iters` x 16 conflict-free 16-byte LDS reads (the GEMM loops' fragment read); bytes per CU =
+ *      waves * 16384 * iters. clk: a live buffer of 32 * waves * CUs bytes that receives, per wave (workgroup-major),
+ *      the shader clock and the 100 MHz reference clock before and after its loop (uint64 each, in that order:
+ *      clock start, clock end, reference start, reference end). */
+int p0k_lds_read_probe(p0k_ctx *ctx, int waves, int iters, uint64_t *clk);
 
 /* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
  *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */

@@ -1,5 +1,5 @@
 // p0k_probe.hip — measurement kernels, not part of the gemm path: the HBM read ceiling the decode GEMV is measured
-// against, and the matrix-core issue ceiling of the MFMA GEMMs (below).
+// against, and the matrix-core issue ceiling and LDS read ceiling of the MFMA GEMMs (below).
 //
 // HBM read ceiling: a plain streaming read of a buffer, by default with the GEMV's launch shape (one 512-thread
 // workgroup per 128-column tile's worth of bytes, 16-byte non-temporal loads, eight in flight per lane; 256-thread
@@ -116,6 +116,48 @@ static hipError_t launch_mfma_valu_r(int valu_per_mfma, unsigned blocks, int ite
 hipError_t launch_mfma_valu(int valu_per_mfma, int random_operands, unsigned blocks, int iters, float *sink, hipStream_t s) {
   return random_operands ? launch_mfma_valu_r<1>(valu_per_mfma, blocks, iters, sink, s)
                          : launch_mfma_valu_r<0>(valu_per_mfma, blocks, iters, sink, s);
+}
+
+}  // namespace p0k
+
+namespace p0k {
+
+// The LDS read ceiling: one workgroup of W waves per CU, every lane reading 16 bytes per ds_read_b128 from a 64 KB
+// array, 16 reads per iteration, each wave's 64 lanes one contiguous KB (no bank conflicts), the GEMM loops' fragment
+// read. Every wave writes the shader clock (s_memtime) and the 100 MHz reference clock (s_memrealtime) before and
+// after its loop to clk[4 (block W + wave) ..], so the host gets both the bytes per clock of a CU and the clock the
+// part ran at.
+template <int W>
+__global__ __launch_bounds__(64 * W) void k_lds_read(uint64_t *clk, int iters) {
+  __shared__ u32x4 s[4096];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  for (int i = tid; i < 4096; i += 64 * W) s[i] = (u32x4){(uint32_t)i, 1u, 2u, 3u};
+  __syncthreads();
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) acc += s[((it * 16 + j) * 64 + lane + wv * 128) & 4095];
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    uint64_t *o = clk + 4 * ((size_t)blockIdx.x * W + wv);
+    o[0] = c0;
+    o[1] = c1;
+    o[2] = r0;
+    o[3] = r1 + (acc.x == 0x9e3779b9u ? acc.y : 0u);    // keeps the reads; practically never changes the value
+  }
+}
+
+hipError_t launch_lds_read(int waves, unsigned blocks, int iters, uint64_t *clk, hipStream_t s) {
+  switch (waves) {
+  case 4: hipLaunchKernelGGL(k_lds_read<4>, dim3(blocks), dim3(256), 0, s, clk, iters); break;
+  case 8: hipLaunchKernelGGL(k_lds_read<8>, dim3(blocks), dim3(512), 0, s, clk, iters); break;
+  case 16: hipLaunchKernelGGL(k_lds_read<16>, dim3(blocks), dim3(1024), 0, s, clk, iters); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace p0k

@@ -623,6 +623,17 @@ int p0k_mfma_valu_probe(p0k_ctx *c, int valu_per_mfma, int waves_per_simd, int i
   return P0K_OK;
 }
 
+int p0k_lds_read_probe(p0k_ctx *c, int waves, int iters, uint64_t *clk) {
+  if (!c) return set_err(P0K_E_ARG, "lds_read_probe: NULL context");
+  if ((waves != 4 && waves != 8 && waves != 16) || iters < 1)
+    return set_err(P0K_E_ARG, "lds_read_probe: waves 4, 8 or 16, iters > 0");
+  if (int r = check_live(c, clk, (uint64_t)32 * (uint64_t)waves * c->tune.cus, "lds_read_probe", "clk")) return r;
+  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
+  hipError_t e = p0k::launch_lds_read(waves, c->tune.cus, iters, clk, c->stream);
+  if (e != hipSuccess) return hip_err(e, "lds_read_probe launch");
+  return P0K_OK;
+}
+
 uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
 
 static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {

@@ -131,7 +131,7 @@ class DeviceInfo(C.Structure):
 EXPORTS = [
     "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
     "p0k_ctx_reload_env", "p0k_ctx_cus", "p0k_gemm_noalloc", "p0k_gemm_noalloc_scratch_bytes", "p0k_stream_read_probe",
-    "p0k_mfma_valu_probe",
+    "p0k_mfma_valu_probe", "p0k_lds_read_probe",
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
     "p0k_attention_check", "p0k_attention", "p0k_attention_flops",
@@ -158,7 +158,7 @@ def lib():
             "p0k_ctx_reload_env": ([P], I), "p0k_ctx_cus": ([P], I),
             "p0k_gemm_noalloc": ([P, C.POINTER(GemmArgs)], I), "p0k_gemm_noalloc_scratch_bytes": ([], U64),
             "p0k_stream_read_probe": ([P, P, U64, P, C.c_uint32, C.c_uint32], I),
-            "p0k_mfma_valu_probe": ([P, I, I, I, I, P], I),
+            "p0k_mfma_valu_probe": ([P, I, I, I, I, P], I), "p0k_lds_read_probe": ([P, I, I, P], I),
             "p0k_device_info_get": ([P, C.POINTER(DeviceInfo)], I),
             "p0k_alloc": ([P, U64, C.POINTER(P)], I), "p0k_free": ([P, P], I), "p0k_drain_pool": ([P], I),
             "p0k_pool_stats_get": ([P, C.POINTER(PoolStats)], I),
@@ -387,6 +387,10 @@ class Device:
         """the matrix-core issue ceiling kernel (see include/p0k.h)"""
         _chk(lib().p0k_mfma_valu_probe(self.ctx, int(valu_per_mfma), int(waves_per_simd), int(iters),
                                        int(bool(random_operands)), sink.ptr))
+
+    def lds_read_probe(self, waves, iters, clk):
+        """the LDS read ceiling kernel (see include/p0k.h); clk: a buffer of 32 * waves * CUs bytes"""
+        _chk(lib().p0k_lds_read_probe(self.ctx, int(waves), int(iters), clk.ptr))
 
     def gemm_raw(self, s):
         _chk(lib().p0k_gemm(self.ctx, C.byref(s)))

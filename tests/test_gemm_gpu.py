@@ -517,6 +517,28 @@ def test_stream_read_probe(dev):
         dev.free(sink)
 
 
+def test_lds_read_probe(dev):
+    """the LDS read probe runs, writes ordered clock pairs for every wave, and refuses out-of-range settings"""
+    cus = dev.cus()
+    clk = dev.buffer(32 * 16 * cus)
+    try:
+        for waves in (4, 8, 16):
+            dev.lds_read_probe(waves, 8, clk)
+            dev.done()
+            t = dev.read(clk, np.uint64, 4 * waves * cus).reshape(-1, 4)
+            assert np.all(t[:, 1] > t[:, 0]) and np.all(t[:, 3] >= t[:, 2]), f"waves {waves}: clocks out of order"
+        with pytest.raises(p0k.P0kError, match="waves 4, 8 or 16"):
+            dev.lds_read_probe(6, 8, clk)
+        small = dev.buffer(32 * 4)
+        try:
+            with pytest.raises(p0k.P0kError):
+                dev.lds_read_probe(4, 8, small)                  # smaller than 32 * waves * CUs bytes
+        finally:
+            dev.free(small)
+    finally:
+        dev.free(clk)
+
+
 def test_mfma_valu_probe(dev):
     """the matrix-core issue probe runs and refuses out-of-range settings"""
     sink = dev.buffer(16)
