@@ -69,6 +69,16 @@ constexpr int mx_ksm() { return MT == 4 ? 8192 : 4096; }
 template <int MT>
 constexpr int mx_lds() { return MT * (mx_ksm<MT>() + 8) * 2 + mx_ksm<MT>() / 32 * MT * 4; }
 
+// The ws column (0..127 inside a tile) that half `h` (a 64-row record block) and row j of it stand for. With the SwiGLU
+// interleave the ws columns alternate gate and up rows, so half 0 takes the even columns (64 consecutive gate rows) and
+// half 1 the odd ones (the matching up rows): every 128-bit load of a wave then covers one whole 1 KB record row-block,
+// as without the interleave, instead of halves of two records far apart (same box: M = 1 13.53 -> 13.44 us, M = 2
+// 14.5 -> 14.25, M = 4 15.09 -> 14.98; k_gemv_mq4 at 8 and 16 rows unchanged).
+// The partials go to LDS in ws column order, so the finish is the same either way.
+__device__ __forceinline__ uint32_t tile_col(const Params &p, uint32_t h, uint32_t j) {
+  return p.epi == E_SWIGLU ? 2u * j + h : 64u * h + j;
+}
+
 // One call's tile without a K split, for the element-wise epilogues (f16, f32, bias, resadd, swiglu): one thread per
 // output element sums the element's K-quarters (in quarter order, as finish() does) and applies the epilogue, so the
 // tile needs no summing pass of its own and every thread has a few instructions of work (the 16-byte-store epilogue
@@ -188,7 +198,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   const int ch = wave / GV_KSUB, sub = wave % GV_KSUB;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
   const uint32_t nB = tile * 128u, kb0 = slice * KS;
-  const uint32_t r = wrow(p, nB + ch * 64 + lane);
+  const uint32_t wsc = tile_col(p, (uint32_t)ch, (uint32_t)lane);
+  const uint32_t r = wrow(p, nB + wsc);
   const uint32_t nuw = KS / UK / GV_KSUB;                      // units of this wave
   const uint32_t u0 = sub * nuw;                               // its first unit inside the slice
 
@@ -421,7 +432,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 
   // the K-quarters meet in LDS
 #pragma unroll
-  for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + ch * 64 + lane] = acc[m];
+  for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + wsc] = acc[m];
   __syncthreads();
   if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
   else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
@@ -483,7 +494,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   uint32_t woff[4], soff[4], rlo[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint32_t r = wrow(p, nB + ch * 64 + (WE == W_Q4 ? lane : 16 * i + l16));
+    const uint32_t r = wrow(p, nB + tile_col(p, (uint32_t)ch, WE == W_Q4 ? (uint32_t)lane : (uint32_t)(16 * i + l16)));
     rlo[i] = r & 1u;
     if constexpr (WE == W_Q4) {
       const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5)) * 1280u;
@@ -673,7 +684,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + ch * 64 + 16 * i + l16] = acc[i][r];
+    for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + tile_col(p, (uint32_t)ch, (uint32_t)(16 * i + l16))] = acc[i][r];
   __syncthreads();
   if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
   else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
@@ -685,7 +696,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 // are copied to LDS while the first weight units are on their way). The same 128-column items as above,
 // but each of the 8 waves covers all 128 columns of one K-eighth, so each X' fragment it loads serves 8 blocks of 16
 // weight rows. Per 32-k unit a wave runs ten v_mfma_f32_16x16x32_f16, every operand in registers:
-//   * lane l loads code rows l and 64 + l of the unit (16 bytes each: one 128-bit load covers 64 rows' 1 KB) and their
+//   * lane l loads code row l of each of the item's two 64-row halves (tile_col; 16 bytes each: one 128-bit load covers
+//     64 rows' 1 KB) and their
 //     (scale, min) words, as the one-row stream does; a 4 x 4 transpose across the four 16-lane groups (two
 //     v_permlane32_swap and two v_permlane16_swap per 64 rows) then gives lane (kc = l / 16, l16 = l % 16) code word
 //     kc of row 16 i + l16 in register i, the B fragment of block i (magic-biased in place: 1024 + q low nibbles,
@@ -723,7 +735,7 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   uint32_t woff[2], soff[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) {
-    const uint32_t r = wrow(p, nB + 64 * h + lane);
+    const uint32_t r = wrow(p, nB + tile_col(p, (uint32_t)h, (uint32_t)lane));
     const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5) + u0) * 1280u;
     woff[h] = rec + (r & 63u) * 16u;
     soff[h] = rec + 1024u + (r & 63u) * 4u;
@@ -847,7 +859,7 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
 #pragma unroll
   for (int i = 0; i < 8; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) sR[(wave * MT + 4 * kc + r) * 128 + 16 * i + l16] = acc[i][r];
+    for (int r = 0; r < 4; r++) sR[(wave * MT + 4 * kc + r) * 128 + tile_col(p, (uint32_t)(i >> 2), (uint32_t)(16 * (i & 3) + l16))] = acc[i][r];
   __syncthreads();
   if (fast_epi(p, S)) finish_fast<MT, MQ_KQ, MQ_NT>(p, sR, nB, tid);
   else finish<MT, MQ_KQ, MQ_NT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
