@@ -63,7 +63,7 @@ MALL = 256 << 20
 # headline's are measured by child rocprofv3 runs at the start of the bench (measure_traffic); for the other
 # workloads, and when rocprofv3 is not available, the figures of the last profiled build are kept here.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (35993, 28), "decode_q4_swiglu_M4": (36149, 112), "decode_q4_swiglu_M16": (36667, 448),
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36010, 28), "decode_q4_swiglu_M4": (36136, 112), "decode_q4_swiglu_M16": (36699, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
