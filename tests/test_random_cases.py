@@ -68,3 +68,34 @@ def test_random_case_matches_oracle(dev, kw):
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on {kern}")
+
+
+def _glu_cases(n=40, seed=20251203):
+    """decode-sized SwiGLU / GeGLU calls with the gate and up row blocks at arbitrary first rows (wr0, and wr1 = wr0 +
+    N / 2 with N / 2 any multiple of 8): the decode kernels give each half of a 128-column item the gate rows and the up
+    rows of its ws columns, which then start anywhere inside a 64-row record"""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        enc = ["q4g32a.t64", "q4g32a.t64", "q8g64s.t64", "f16"][rng.integers(4)]
+        M = int([1, 1, 2, 3, 4, 4, 5, 8, 11, 16][rng.integers(10)])
+        K = int(256 * rng.integers(1, 5)) if enc != "q8g64s.t64" else int(512 * rng.integers(1, 3))
+        out.append(dict(enc=enc, xmode=["f16", "f16", "rms"][rng.integers(3)], epi="swiglu", M=M, K=K,
+                        N=16 * int(rng.integers(1, 40)), wr0=int([0, 1, 5, 63, 64, 100][rng.integers(6)]),
+                        act=["silu", "gelu"][rng.integers(2)], bias=bool(rng.integers(2)),
+                        seed=int(rng.integers(1, 1 << 20))))
+    return out
+
+
+GLU_CASES = _glu_cases()
+
+
+@pytest.mark.parametrize("kw", GLU_CASES, ids=[f"{i:02d}-{k['enc'][:2]}-M{k['M']}-N{k['N']}-K{k['K']}-wr0{k['wr0']}"
+                                               for i, k in enumerate(GLU_CASES)])
+def test_random_glu_case_matches_oracle(dev, kw):
+    c = make_case(**kw)
+    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    print(f"[p0k-test] random GLU case {kw} kernel={kern}", flush=True)
+    got = c.run_device(dev)
+    want = c.run_oracle()
+    assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on {kern}")
