@@ -56,6 +56,18 @@ def test_valid_cases_pass_check():
     p0k.check(host_args(make_conv3_case()))
 
 
+def test_empty_calls_pass_check():
+    """M = 0 or N = 0: the reference makes zero tiles and dispatches nothing (src/ops/gemm.js:312-319); the checks of
+    the other arguments still apply"""
+    for M, N in [(0, 256), (4, 0), (0, 0)]:
+        a = host_args(make_case(enc="q4g32a.t64", M=4, N=256, K=256))
+        a.update(M=M, N=N)
+        p0k.check(a)
+    a = host_args(make_case(enc="q4g32a.t64", M=4, N=256, K=256))
+    a.update(M=0, K=48)
+    expect_error(a, "K must be a multiple of 32")
+
+
 def test_reference_errors():
     c = make_case()
     a = host_args(c)

@@ -158,6 +158,24 @@ def test_matrix_core_stream_long_k(dev, M, K, slices, monkeypatch):
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"stream M={M} K={K}")
 
 
+@pytest.mark.parametrize("M,N", [(0, 256), (4, 0), (0, 0)])
+def test_empty_calls_write_nothing(dev, M, N):
+    """src/ops/gemm.js:312-319: M = 0 or N = 0 makes zero tiles, so the call dispatches nothing and returns 2 M N K
+    (0); here the call is validated and returns without a launch, leaving the output as it was."""
+    c = make_case(enc="q4g32a.t64", M=4, N=256, K=256, seed=61)
+    d = {k: dev.upload(v) for k, v in c.bufs.items()}
+    try:
+        before = dev.read(d[c.out], np.uint8)
+        a = c.args(lambda n: d[n])
+        a.update(M=M, N=N)
+        assert dev.gemm(a) == 0
+        dev.done()
+        assert np.array_equal(dev.read(d[c.out], np.uint8), before)
+    finally:
+        for b in d.values():
+            dev.free(b)
+
+
 # ------------------------------------------------------------------------------------------------ dequantisation
 def _adversarial_q4(rows, K, seed):
     """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
