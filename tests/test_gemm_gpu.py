@@ -176,6 +176,33 @@ def test_empty_calls_write_nothing(dev, M, N):
             dev.free(b)
 
 
+@pytest.mark.parametrize("enc,M", [("q4g32a.t64", 1), ("q4g32a.t64", 4), ("q8g64s.t64", 8), ("q4g32a.t64", 300),
+                                   ("f16", 300)])
+def test_weights_past_4gib_in_a_large_buffer(dev, enc, M):
+    """A weight tensor stored 4.25 GiB into one large device buffer (a model shard): `w.off` is folded into the base
+    the kernels address from, so their 32-bit offsets only span the tensor itself (the reference binds such a window
+    from the 256-byte boundary before it, src/ops/gemm.js:289-296)."""
+    c = make_case(enc=enc, epi="f16", M=M, N=256, K=512, seed=71)
+    off = (4 << 30) + (256 << 20)
+    big = dev.buffer(off + c.bufs["w"].nbytes)
+    d = {}
+    try:
+        dev.upload(c.bufs["w"], dst=big, dst_off=off)
+        d = {k: dev.upload(v) for k, v in c.bufs.items() if k != "w"}
+        a = c.args(lambda n: big if n == "w" else d[n])
+        a["w"]["off"] = off
+        dev.gemm(a)
+        dev.done()
+        out = c.bufs[c.out]
+        got = dev.read(d[c.out], out.dtype, out.size)
+        assert_close(got, c.run_oracle(), fp16=got.dtype == np.uint16, what=f"{enc} M={M} at 4.25 GiB")
+    finally:
+        for b in d.values():
+            dev.free(b)
+        dev.free(big)
+        dev.drain_pool()
+
+
 # ------------------------------------------------------------------------------------------------ dequantisation
 def _adversarial_q4(rows, K, seed):
     """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
