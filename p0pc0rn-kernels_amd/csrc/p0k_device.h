@@ -74,6 +74,16 @@ __device__ __forceinline__ u32x2 sload64(srsrc r, uint32_t off) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, SC0_NT));
 }
 __device__ __forceinline__ uint32_t sload32(srsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, SC0_NT); }
+// System-coherent 16-byte vector accesses (cache policy sc0 sc1: they skip the per-XCD L2s, so workgroups on different
+// XCDs exchange data through memory without any L2 writeback or invalidation; a store counts as done only once it is
+// there): the split-K partials of the decode.
+constexpr int SC0_SC1 = 17;
+__device__ __forceinline__ void sys_store128(srsrc r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, SC0_SC1);
+}
+__device__ __forceinline__ u32x4 sys_load128(srsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, SC0_SC1));
+}
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 

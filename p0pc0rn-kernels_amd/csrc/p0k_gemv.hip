@@ -148,12 +148,16 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
     // partial tile -> workspace [slice][m][ws column, padded to whole tiles]. The partials, the counter and the reads
     // of the last item all go to the memory side (system-coherent accesses that skip the per-XCD L2s), so items on
     // different XCDs meet without any L2 writeback or invalidation: a store is acknowledged only once it is there,
-    // and every thread waits for its acknowledgements before the barrier that precedes the counter update.
+    // and every thread waits for its acknowledgements before the barrier that precedes the counter update. Partials
+    // move in 16-byte vectors; workspace offsets are 32-bit (the host keeps the workspace below 4 GiB). What a split
+    // costs is the chain at the end of the last item of a tile (store, acknowledgement, counter, loads: each a trip to
+    // memory), about 3 us per call whatever the partials' size, so the host splits only to fill the GPU.
     const uint32_t Np = gridDim.x / S * 128u;
     const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
-    for (uint32_t t = tid; t < rows * 128; t += NT) {
-      uint32_t m = t >> 7, c = t & 127;
-      __hip_atomic_store(part + ((size_t)slice * p.M + m) * Np + nB + c, sR[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const srsrc pr = stream_rsrc((const uint8_t *)part);
+    for (uint32_t t = tid; t < rows * 32; t += NT) {
+      const uint32_t m = t >> 5, c = (t & 31) * 4;
+      sys_store128(pr, ((slice * p.M + m) * Np + nB + c) * 4u, *(const u32x4 *)(sR + m * 128 + c));
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -163,13 +167,11 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
     }
     __syncthreads();
     if (!sLast) return;
-    for (uint32_t t = tid; t < rows * 128; t += NT) {
-      uint32_t m = t >> 7, c = t & 127;
-      const float *src = part + (size_t)m * Np + nB + c;
-      float s = 0.0f;
-      for (uint32_t q = 0; q < S; q++)
-        s += __hip_atomic_load(src + (size_t)q * p.M * Np, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      sR[t] = s;
+    for (uint32_t t = tid; t < rows * 32; t += NT) {
+      const uint32_t m = t >> 5, c = (t & 31) * 4;
+      f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (uint32_t q = 0; q < S; q++) s += __builtin_bit_cast(f32x4, sys_load128(pr, ((q * p.M + m) * Np + nB + c) * 4u));
+      *(f32x4 *)(sR + m * 128 + c) = s;
     }
     if (tid == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();

@@ -469,6 +469,7 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
     if (plan.S > 1) {
       if (tiles > p0k_ctx::WS_COUNTERS) return set_err(P0K_E_UNSUPPORTED, "gemm: N too large for the decode workspace");
       const uint64_t need = (uint64_t)plan.S * a->M * tiles * 128u * sizeof(float);
+      if (need >= (1ull << 32)) return set_err(P0K_E_UNSUPPORTED, "gemm: decode split workspace of 4 GiB or more");
       if (int rr = ws.part(need, &part)) return rr;
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, part, ws.counters(), plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF,
