@@ -57,6 +57,7 @@ Tuning tuning_from_env(unsigned cus) {
   if (const char *ov = getenv("P0K_GEMV_MQ4")) t.gemv_mq4 = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_GEMV_SLICES")) t.gemv_slices = (unsigned)std::max(0, atoi(ov));
   if (const char *ov = getenv("P0K_GEMV_MX")) t.gemv_mx = (unsigned)std::max(0, atoi(ov));
+  if (const char *ov = getenv("P0K_GEMV_NARROW")) t.gemv_narrow = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_MFMA_KERNEL")) t.mfma_reg = strcmp(ov, "reg") == 0;
   if (const char *ov = getenv("P0K_MFMA_TILE")) {
     unsigned tm = 0, tn = 0;
@@ -249,7 +250,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M)
   int kernel = K_MFMA;
   unsigned S = 0, KS = 0;
-  bool mx = false;
+  bool mx = false, narrow = false;
   if (M <= (uint32_t)GEMV_MAX_M && (xm == P0K_X_F16 || xf32) && M > 0) {
     // the GEMV reads q8 in whole 64-k records and f16 rows with 16-byte loads only
     // and addresses the tensor with 32-bit offsets
@@ -267,8 +268,20 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       mx = we == P0K_ENC_Q4G32A_T64 && M >= 2 && M <= tune.gemv_mx;
       if (mx) mf = false;
       gemv_split(p, we, tune.cus, mf, mx, &S, &KS);
+      // q4 with up to 4 rows whose 128-column tiles fill only half the GPU (S = 2 above): 64-column items with
+      // 8 K-eighths each instead, no K split (plain q4 N 14336, 112 tiles: 8.1 vs 9.7 us per call; the split's
+      // store-acknowledge-count-load chain at the end costs about 3 us)
+      const uint32_t tiles128 = (N + 127) / 128;
+      if (tune.gemv_narrow && !mf && S == 2 && we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS &&
+          epi != P0K_EPI_ONORMGATE && 2 * tiles128 >= tune.cus * 7u / 8u && K <= gemv_ks_max(M, we, mf, mx) &&
+          K % 256 == 0) {
+        narrow = true;
+        S = 1;
+        KS = K;
+      }
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
       if (tune.gemv_slices) {
+        narrow = false;
         unsigned s2 = tune.gemv_slices, quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
         if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
@@ -277,7 +290,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   }
   if (out) *out = p;
   if (plan) {
-    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = 128; plan->mx = mx;
+    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = narrow ? 64 : 128; plan->mx = mx; plan->narrow = narrow;
     // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
     if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes) && !tune.mfma_reg) kernel = plan->kernel = K_MFMA_DMA;
     if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, tune.cus, &plan->bm, &plan->bn);

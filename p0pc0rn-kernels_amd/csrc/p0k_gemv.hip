@@ -83,8 +83,9 @@ __device__ __forceinline__ uint32_t tile_col(const Params &p, uint32_t h, uint32
 // output element sums the element's K-quarters (in quarter order, as finish() does) and applies the epilogue, so the
 // tile needs no summing pass of its own and every thread has a few instructions of work (the 16-byte-store epilogue
 // of finish() gives 8 threads 8 outputs each per row, a long serial tail at the end of the stream).
-template <int MT, int KQ = GV_KSUB, int NT = GV_NT>
+template <int MT, int KQ = GV_KSUB, int NT = GV_NT, int TW = 128>
 __device__ __forceinline__ void finish_fast(const Params &p, const float *sR, uint32_t nB, int tid) {
+  constexpr uint32_t HW = TW / 2;
   const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
   auto qsum = [&](uint32_t m, uint32_t c) {
     float s = sR[m * 128 + c];
@@ -95,8 +96,8 @@ __device__ __forceinline__ void finish_fast(const Params &p, const float *sR, ui
   if (p.epi == E_SWIGLU) {                                                        // gemm.js:204-210
     const uint32_t Nout = p.N >> 1;
     const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
-    for (uint32_t t = tid; t < rows * 64; t += NT) {
-      const uint32_t m = t >> 6, c = t & 63, o = (nB >> 1) + c;
+    for (uint32_t t = tid; t < rows * HW; t += NT) {
+      const uint32_t m = t / HW, c = t % HW, o = (nB >> 1) + c;
       if (o >= Nout) continue;
       float gt = qsum(m, 2 * c), u = qsum(m, 2 * c + 1);
       if (bias) { gt += p.BV[p.bvOff + o]; u += p.BV[p.bvOff + p.bvUp + o]; }
@@ -104,8 +105,8 @@ __device__ __forceinline__ void finish_fast(const Params &p, const float *sR, ui
     }
     return;
   }
-  for (uint32_t t = tid; t < rows * 128; t += NT) {
-    const uint32_t m = t >> 7, c = t & 127, col = nB + c;
+  for (uint32_t t = tid; t < rows * TW; t += NT) {
+    const uint32_t m = t / TW, c = t % TW, col = nB + c;
     if (col >= p.N) continue;
     const float v = qsum(m, c);
     const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
@@ -179,17 +180,21 @@ __device__ __forceinline__ void finish(const Params &p, float *sR, float *part, 
   epilogue<NT>(p, sR, 128, MT, 0u, nB, tid);
 }
 
-template <int WE, int XM, int MT>
+// NARROW: items of 64 ws columns (one record block) with the 8 waves as 8 K-eighths, for calls whose 128-column
+// tiles would fill only half the GPU: twice the items without a K split (S = 1 and the element-wise epilogues only).
+template <int WE, int XM, int MT, bool NARROW = false>
 __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
+  static_assert(!NARROW || (WE == W_Q4 && MT <= 4), "narrow items: q4 with up to 4 rows");
+  constexpr int KQ = NARROW ? 2 * GV_KSUB : GV_KSUB, TW = NARROW ? 64 : 128;   // K parts per item, item width
   constexpr bool MX = gv_mx<WE, MT>();
   constexpr int UK = Unit<WE>::UK, PF = MX ? P0K_MX_PF : Unit<WE>::PF, KSM = MX ? mx_ksm<MT>() : ks_max<MT>(), NGM = KSM / UK;
   constexpr int XSTR = MX ? KSM + 8 : KSM;                     // halves per staged X' row
   constexpr int LDSB = MX ? mx_lds<MT>() : GV_LDS;
-  static_assert(GV_KSUB * MT * 128 * 4 <= LDSB, "partials must fit the staging buffer");
-  // one or two rows: the partials get their own 2-4 KB, so the waves write them as they finish their streams without
+  static_assert(KQ * MT * 128 * 4 <= LDSB, "partials must fit the staging buffer");
+  // one or two rows: the partials get their own 2-8 KB, so the waves write them as they finish their streams without
   // waiting for each other; more rows: the partials reuse the X' buffer after a barrier
   constexpr bool SEP = MT <= 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[LDSB + (SEP ? GV_KSUB * MT * 128 * 4 : 0)];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[LDSB + (SEP ? KQ * MT * 128 * 4 : 0)];
   __shared__ uint32_t sLast;
   f16 *sX = (f16 *)smem;                                       // [MT][XSTR] X', pair order of the encoding
   f32x2 *sG = (f32x2 *)(smem + MT * XSTR * 2);                 // [MT][KSM / UK] (Xlo, Xhi) per unit
@@ -197,12 +202,12 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   float *sR = (float *)(smem + (SEP ? GV_LDS : 0));            // after the stream: partials
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ch = wave / GV_KSUB, sub = wave % GV_KSUB;
+  const int ch = NARROW ? 0 : wave / GV_KSUB, sub = NARROW ? wave : wave % GV_KSUB;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
-  const uint32_t nB = tile * 128u, kb0 = slice * KS;
-  const uint32_t wsc = tile_col(p, (uint32_t)ch, (uint32_t)lane);
+  const uint32_t nB = tile * (uint32_t)TW, kb0 = slice * KS;
+  const uint32_t wsc = NARROW ? (uint32_t)lane : tile_col(p, (uint32_t)ch, (uint32_t)lane);
   const uint32_t r = wrow(p, nB + wsc);
-  const uint32_t nuw = KS / UK / GV_KSUB;                      // units of this wave
+  const uint32_t nuw = KS / UK / KQ;                           // units of this wave
   const uint32_t u0 = sub * nuw;                               // its first unit inside the slice
 
   // byte offset of this lane's first unit from the tensor start: 32-bit (the host routes tensors of 4 GiB or more to
@@ -436,7 +441,8 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 #pragma unroll
   for (int m = 0; m < MT; m++) sR[(sub * MT + m) * 128 + wsc] = acc[m];
   __syncthreads();
-  if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
+  if constexpr (NARROW) finish_fast<MT, KQ, GV_NT, TW>(p, sR, nB, tid);     // (the host sends only S = 1 here)
+  else if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
   else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
@@ -899,15 +905,24 @@ void gemv_split(const Params &p, int we, unsigned cus, bool mf, bool mx, unsigne
 }
 
 template <int WE, int XM, int MT>
-static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s) {
+static hipError_t launch3(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s,
+                          bool narrow) {
   if (KS > (uint32_t)(gv_mx<WE, MT>() ? mx_ksm<MT>() : ks_max<MT>())) return hipErrorInvalidValue;
+  if constexpr (WE == W_Q4 && MT <= 4) {
+    if (narrow) {
+      if (S != 1 || p.epi == E_HEADS || p.epi == E_ONORMGATE) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((k_gemv<WE, XM, MT, true>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+      return hipGetLastError();
+    }
+  }
+  if (narrow) return hipErrorInvalidValue;
   dim3 grid(((p.N + 127) / 128) * S);
   hipLaunchKernelGGL((k_gemv<WE, XM, MT>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
   return hipGetLastError();
 }
 template <int WE, int XM>
 static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s, bool mf,
-                          bool mq4, bool mx) {
+                          bool mq4, bool mx, bool narrow) {
   if (mf) {
     if (KS > (uint32_t)MF_KSM) return hipErrorInvalidValue;
     dim3 grid(((p.N + 127) / 128) * S);
@@ -920,32 +935,33 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
     return hipGetLastError();
   }
   switch (stream_mt(p.M, WE, mx)) {
-  case 1: return launch3<WE, XM, 1>(p, part, cnt, S, KS, s);
-  case 2: return launch3<WE, XM, 2>(p, part, cnt, S, KS, s);
-  case 4: return launch3<WE, XM, 4>(p, part, cnt, S, KS, s);
-  case 8: return launch3<WE, XM, 8>(p, part, cnt, S, KS, s);
+  case 1: return launch3<WE, XM, 1>(p, part, cnt, S, KS, s, narrow);
+  case 2: return launch3<WE, XM, 2>(p, part, cnt, S, KS, s, narrow);
+  case 4: return launch3<WE, XM, 4>(p, part, cnt, S, KS, s, narrow);
+  case 8: return launch3<WE, XM, 8>(p, part, cnt, S, KS, s, narrow);
   }
-  return launch3<WE, XM, 16>(p, part, cnt, S, KS, s);
+  return launch3<WE, XM, 16>(p, part, cnt, S, KS, s, narrow);
 }
 template <int WE>
 static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS, hipStream_t s,
-                          bool mf, bool mq4, bool mx) {
+                          bool mf, bool mq4, bool mx, bool narrow) {
   switch (xm) {
-  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf, mq4, mx);
-  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf, mq4, mx);
-  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf, mq4, mx);
+  case X_F16: return launch2<WE, X_F16>(p, part, cnt, S, KS, s, mf, mq4, mx, narrow);
+  case X_LNMOD: return launch2<WE, X_LNMOD>(p, part, cnt, S, KS, s, mf, mq4, mx, narrow);
+  case X_RMS: return launch2<WE, X_RMS>(p, part, cnt, S, KS, s, mf, mq4, mx, narrow);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
-                       hipStream_t s, bool mf, bool mq4, bool mx) {
+                       hipStream_t s, bool mf, bool mq4, bool mx, bool narrow) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
+  if (narrow && (mf || we != W_Q4 || S != 1)) return hipErrorInvalidValue;
   switch (we) {
-  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
-  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
-  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf, mq4, mx);
+  case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);
+  case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);
+  case W_F16: return launch1<W_F16>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);
   }
   return hipErrorInvalidValue;
 }

@@ -8,7 +8,7 @@ namespace p0k {
 struct Params;
 enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2, K_MFMA_DMA = 3 };
 // kernel choice of one call: GEMV items are (128-column tile) x (K slice of KS), S slices per tile
-struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; bool mx; };
+struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; bool mx, narrow; };
 // What the kernel choice depends on besides the call: the device's CU count and the P0K_* tuning switches of the
 // environment. A context reads them once (at creation and on p0k_ctx_reload_env); calls without a context read
 // them on the spot.
@@ -18,6 +18,7 @@ struct Tuning {
   bool gemv_mq4 = true;        // P0K_GEMV_MQ4=0: q4 matrix-core decode with X' staged in LDS (k_gemv_mf)
   unsigned gemv_slices = 0;    // P0K_GEMV_SLICES=n: decode K slices (0: not set)
   unsigned gemv_mx = 4;        // P0K_GEMV_MX=n: q4 decode with 2..n rows on the stream kernel's matrix-core form
+  bool gemv_narrow = true;     // P0K_GEMV_NARROW=0: no 64-column decode items (a K split fills the GPU instead)
   bool mfma_reg = false;       // P0K_MFMA_KERNEL=reg: the register-staged MFMA kernel
   unsigned tile_m = 0, tile_n = 0;   // P0K_MFMA_TILE=MxN
   bool dma_tail = true;        // P0K_DMA_TAIL=0: one launch for a mostly empty last round

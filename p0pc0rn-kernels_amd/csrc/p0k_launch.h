@@ -28,11 +28,12 @@ hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigne
 // decode GEMV (M <= 16, prologue f16 / rms / lnmod): items of 128 ws columns x K/S; S > 1 needs the workspace
 // (part: S*M*N floats, cnt: one zeroed counter per 128-column tile). mf: the matrix-core variant (2 <= M <= 16);
 // mq4: with q4 weights, its form without X' staging (k_gemv_mq4); mx: q4 at M = 2 takes the stream kernel's
-// matrix-core form (4-row tile) instead of its dot-product form (q4 with 3..16 rows on the stream kernel always does)
+// matrix-core form (4-row tile) instead of its dot-product form (q4 with 3..16 rows on the stream kernel always does);
+// narrow: the stream kernel (q4, M <= 4, S = 1, element-wise epilogues) over items of 64 columns instead of 128
 void gemv_split(const Params &p, int we, unsigned cus, bool mf, bool mx, unsigned *S, unsigned *KS);
 unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx);   // longest K slice one item stages
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s,
-                       bool mf, bool mq4, bool mx);
+                       bool mf, bool mq4, bool mx, bool narrow);
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);

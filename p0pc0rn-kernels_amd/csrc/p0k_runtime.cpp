@@ -473,7 +473,7 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
       if (int rr = ws.part(need, &part)) return rr;
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, part, ws.counters(), plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF,
-                          c->tune.gemv_mq4, plan.mx);
+                          c->tune.gemv_mq4, plan.mx, plan.narrow);
   } else if (plan.kernel == p0k::K_MFMA_DMA && plan.xm == P0K_X_CONV3) {
     p.Z = (const uint8_t *)ws.zero();
     if (p.flags & p0k::F_PN) {

@@ -284,7 +284,7 @@ class Buffer:
         self.ptr, self.size, self.dev = ptr, size, dev
 
 
-TUNING_SWITCHES = ("P0K_MFMA_TILE", "P0K_MFMA_KERNEL", "P0K_DMA_TAIL", "P0K_GEMV_MF", "P0K_GEMV_MQ4", "P0K_GEMV_MX", "P0K_GEMV_SLICES",
+TUNING_SWITCHES = ("P0K_MFMA_TILE", "P0K_MFMA_KERNEL", "P0K_DMA_TAIL", "P0K_GEMV_MF", "P0K_GEMV_MQ4", "P0K_GEMV_MX", "P0K_GEMV_NARROW", "P0K_GEMV_SLICES",
                    "P0K_ATTN_BQ")
 
 
