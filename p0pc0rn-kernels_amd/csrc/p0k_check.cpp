@@ -268,13 +268,16 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       mx = we == P0K_ENC_Q4G32A_T64 && M >= 2 && M <= tune.gemv_mx;
       if (mx) mf = false;
       gemv_split(p, we, tune.cus, mf, mx, &S, &KS);
-      // q4 with up to 4 rows whose 128-column tiles fill only half the GPU (S = 2 above): 64-column items with
-      // 8 K-eighths each instead, no K split (plain q4 N 14336, 112 tiles: 8.1 vs 9.7 us per call; the split's
-      // store-acknowledge-count-load chain at the end costs about 3 us)
+      // q4 with up to 4 rows that the planner would split: 64-column items with 8 K-eighths each instead, no K split
+      // (the split's store-acknowledge-count-load chain at the end costs about 3 us), when those items fill the GPU
+      // (plain q4 N 14336, 112 tiles: 8.1 vs 9.7 us per call) or each one's stream is short (40 K bytes, at most
+      // 256 KB: one item per CU then streams at about 43 GB/s, its ring's bytes in flight over the memory latency;
+      // N 4096 / 6144 / 8192 with K 4096: 6.2 / 6.5 / 6.5 against 8.9 / 10.1 / 8.7 us split; N 4096 K 14336: 15.7
+      // against 12.0, so long K keeps the split)
       const uint32_t tiles128 = (N + 127) / 128;
-      if (tune.gemv_narrow && !mf && S == 2 && we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS &&
-          epi != P0K_EPI_ONORMGATE && 2 * tiles128 >= tune.cus * 7u / 8u && K <= gemv_ks_max(M, we, mf, mx) &&
-          K % 256 == 0) {
+      const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u, short_k = (uint64_t)K * 40u <= 256u * 1024u;
+      if (tune.gemv_narrow && !mf && S >= 2 && we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS &&
+          epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) && K % 256 == 0) {
         narrow = true;
         S = 1;
         KS = K;
