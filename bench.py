@@ -92,10 +92,11 @@ class Workload:
         self.M, self.args, self.bufs, self.extra, self.kind = M, args, bufs, extra or {}, kind
 
 
-def decode_q4(dev, M, copies=None, glu=True):
+def decode_q4(dev, M, copies=None, glu=True, n_out=14336):
     """q4 GEMV decode, out 14336 with SwiGLU (weight rows [gate 14336 | up 14336]), K 4096; glu=False:
-    the plain q4 GEMV N 14336 (36.7 MB of weights) with the f16 epilogue."""
-    N_out, K = 14336, 4096
+    the plain q4 GEMV N n_out with the f16 epilogue (14336: 36.7 MB of weights; 4096: the same model's attention
+    projection, 10.5 MB)."""
+    N_out, K = n_out, 4096
     rows = 2 * N_out if glu else N_out
     r = rng(1)
     W = (r.standard_normal((rows, K), dtype=np.float32) * np.float32(0.02))
@@ -115,7 +116,8 @@ def decode_q4(dev, M, copies=None, glu=True):
             del a["wr1"]
     nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
     if not glu:
-        return Workload(f"decode_q4_plain_M{M}", f"q4 GEMV, M={M}, N={N_out}, K={K}, f16 epilogue", "hbm",
+        name = f"decode_q4_plain_M{M}" if N_out == 14336 else f"decode_q4_plain_N{N_out}_M{M}"
+        return Workload(name, f"q4 GEMV, M={M}, N={N_out}, K={K}, f16 epilogue", "hbm",
                         2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
     return Workload(f"decode_q4_swiglu_M{M}", f"q4 GEMV + SwiGLU, M={M}, out {N_out}, weight rows {rows}, K={K}",
                     "hbm", 2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
@@ -282,6 +284,7 @@ BUILDERS = {
     "decode1": lambda d: decode_q4(d, 1), "hbm_ceiling": hbm_ceiling, "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
     "decode2": lambda d: decode_q4(d, 2), "decode8": lambda d: decode_q4(d, 8),
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
+    "decode1_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
     "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
 }
