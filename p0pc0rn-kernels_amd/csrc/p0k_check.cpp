@@ -276,8 +276,10 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // against 12.0, so long K keeps the split)
       const uint32_t tiles128 = (N + 127) / 128;
       const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u, short_k = (uint64_t)K * 40u <= 256u * 1024u;
-      if (tune.gemv_narrow && !mf && S >= 2 && we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS &&
-          epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) && K % 256 == 0) {
+      // (k_gemv_mq4, q4 with 5..16 rows, the same with items of one 64-row half)
+      if (tune.gemv_narrow && (!mf || tune.gemv_mq4) && S >= 2 && we == P0K_ENC_Q4G32A_T64 && (mf || M <= 4) &&
+          epi != P0K_EPI_HEADS && epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) &&
+          K % 256 == 0) {
         narrow = true;
         S = 1;
         KS = K;

@@ -724,9 +724,11 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 constexpr int MQ_KQ = 8, MQ_NT = 64 * MQ_KQ, MQ_PF = 3;     // waves = K parts of an item; units in flight per wave
 constexpr int MQ_XP = MF_KSM * 2 + 16;                       // LDS bytes per staged X row
 constexpr int MQ_LDS = 16 * MQ_XP > MQ_KQ * 16 * 128 * 4 ? 16 * MQ_XP : MQ_KQ * 16 * 128 * 4;
-template <int XM, bool XL>
+// NARROW: items of 64 ws columns (one half: 4 blocks of 16 rows), S = 1 and the element-wise epilogues only, for calls
+// whose 128-column items the planner would split (the same rule as the one-row stream's 64-column items)
+template <int XM, bool XL, bool NARROW = false>
 __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
-  constexpr int MT = 16, PF = MQ_PF;
+  constexpr int MT = 16, PF = MQ_PF, NH = NARROW ? 1 : 2, TW = 64 * NH;   // halves (64-row blocks) per item
   static_assert(!XL || XM == X_F16, "X rows are copied as they are only without a prologue");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[XL ? MQ_LDS : MQ_KQ * MT * 128 * 4];
   __shared__ uint32_t sLast;
@@ -735,15 +737,15 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, kc = lane >> 4;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
-  const uint32_t nB = tile * 128u, kb0 = slice * KS;
+  const uint32_t nB = tile * (uint32_t)TW, kb0 = slice * KS;
   const uint32_t nu = KS / 32u, u0 = wave * nu / MQ_KQ, nuw = (wave + 1) * nu / MQ_KQ - u0;   // units of this wave
 
   // this lane's weight rows (lane and 64 + lane of the tile): byte offsets of their code rows and (scale, min) words in
   // the wave's first unit (32-bit: tensors of 4 GiB or more take the MFMA GEMM)
-  uint32_t woff[2], soff[2];
+  uint32_t woff[NH], soff[NH];
 #pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const uint32_t r = wrow(p, nB + tile_col(p, (uint32_t)h, (uint32_t)lane));
+  for (int h = 0; h < NH; h++) {
+    const uint32_t r = wrow(p, nB + (NARROW ? (uint32_t)lane : tile_col(p, (uint32_t)h, (uint32_t)lane)));
     const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5) + u0) * 1280u;
     woff[h] = rec + (r & 63u) * 16u;
     soff[h] = rec + 1024u + (r & 63u) * 4u;
@@ -766,14 +768,14 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
     }
   }
 
-  struct U { u32x4 code[2]; uint32_t sm[2]; u32x4 x; };
+  struct U { u32x4 code[NH]; uint32_t sm[NH]; u32x4 x; };
   const srsrc wr = stream_rsrc(p.W);
   auto load = [&](U &u, uint32_t j) __attribute__((always_inline)) {
     const uint32_t du = j * 1280u;
 #pragma unroll
-    for (int h = 0; h < 2; h++) u.code[h] = sload128(wr, woff[h] + du);
+    for (int h = 0; h < NH; h++) u.code[h] = sload128(wr, woff[h] + du);
 #pragma unroll
-    for (int h = 0; h < 2; h++) u.sm[h] = sload32(wr, soff[h] + du);
+    for (int h = 0; h < NH; h++) u.sm[h] = sload32(wr, soff[h] + du);
     if constexpr (!XL) u.x = xload8<XM>(p, xrow, RowCtx{0, 0, 0}, xk0 + j * 32u);
   };
   // the A fragment of the wave's unit j
@@ -791,9 +793,9 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
   const f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  f32x4 acc[8];
+  f32x4 acc[4 * NH];
 #pragma unroll
-  for (int i = 0; i < 8; i++) acc[i] = z4;
+  for (int i = 0; i < 4 * NH; i++) acc[i] = z4;
 
   auto compute = [&](const U &u, uint32_t j) __attribute__((always_inline)) {
     u32x4 xv = xperm<W_Q4>(xfrag(u, j));
@@ -803,7 +805,7 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
     const f32x4 ng1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bneg, z4, 0, 0, 0);
     const f32x4 g2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bg2, z4, 0, 0, 0);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < NH; h++) {
       // the 4 x 4 transpose of (16-lane group, code word): word kc of row 64 h + 16 i + l16 into register i
       uint32_t w[4];
       {
@@ -844,7 +846,8 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   }
   if constexpr (XL) {
     // the X copy is older than the ring's loads (loads complete in order): wait for it alone, then for every wave's
-    __builtin_amdgcn_s_waitcnt((4 * PF & 15) | (((4 * PF) >> 4) << 14) | 0x0f70);   // vmcnt(4 PF): 4 loads per unit
+    constexpr int LPU = 2 * NH;                                // loads per unit
+    __builtin_amdgcn_s_waitcnt((LPU * PF & 15) | (((LPU * PF) >> 4) << 14) | 0x0f70);   // vmcnt(LPU PF)
     __syncthreads();
   }
   uint32_t j0 = 0;
@@ -865,11 +868,14 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
 
   // D[m = 4 kc + r][row 16 i + l16] of the tile's rows 64 h + ...; the K-eighths meet in LDS
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < 4 * NH; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) sR[(wave * MT + 4 * kc + r) * 128 + tile_col(p, (uint32_t)(i >> 2), (uint32_t)(16 * (i & 3) + l16))] = acc[i][r];
+    for (int r = 0; r < 4; r++)
+      sR[(wave * MT + 4 * kc + r) * 128 +
+         (NARROW ? (uint32_t)(16 * i + l16) : tile_col(p, (uint32_t)(i >> 2), (uint32_t)(16 * (i & 3) + l16)))] = acc[i][r];
   __syncthreads();
-  if (fast_epi(p, S)) finish_fast<MT, MQ_KQ, MQ_NT>(p, sR, nB, tid);
+  if constexpr (NARROW) finish_fast<MT, MQ_KQ, MQ_NT, TW>(p, sR, nB, tid);   // (the host sends only S = 1 here)
+  else if (fast_epi(p, S)) finish_fast<MT, MQ_KQ, MQ_NT>(p, sR, nB, tid);
   else finish<MT, MQ_KQ, MQ_NT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
@@ -927,10 +933,18 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
     if (KS > (uint32_t)MF_KSM) return hipErrorInvalidValue;
     dim3 grid(((p.N + 127) / 128) * S);
     if (WE == W_Q4 && mq4) {
+      if (narrow) {
+        if (S != 1 || p.epi == E_HEADS || p.epi == E_ONORMGATE) return hipErrorInvalidValue;
+        const dim3 g64((p.N + 63) / 64);
+        if (XM == X_F16 && (p.flags & F_XALIGN8)) hipLaunchKernelGGL((k_gemv_mq4<X_F16, true, true>), g64, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
+        else hipLaunchKernelGGL((k_gemv_mq4<XM, false, true>), g64, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
+        return hipGetLastError();
+      }
       if (XM == X_F16 && (p.flags & F_XALIGN8)) hipLaunchKernelGGL((k_gemv_mq4<X_F16, true>), grid, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
       else hipLaunchKernelGGL((k_gemv_mq4<XM, false>), grid, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
       return hipGetLastError();
     }
+    if (narrow) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
   }
@@ -957,7 +971,7 @@ hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *c
                        hipStream_t s, bool mf, bool mq4, bool mx, bool narrow) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
-  if (narrow && (mf || we != W_Q4 || S != 1)) return hipErrorInvalidValue;
+  if (narrow && (we != W_Q4 || S != 1 || (mf && !mq4))) return hipErrorInvalidValue;
   switch (we) {
   case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);
   case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);

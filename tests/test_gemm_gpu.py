@@ -206,16 +206,18 @@ def test_weights_past_4gib_in_a_large_buffer(dev, enc, M):
 @pytest.mark.parametrize("narrow", [True, False])
 @pytest.mark.parametrize("epi,M,N,K", [("swiglu", 2, 14400, 1024), ("resadd", 3, 16000, 512), ("bias", 4, 14592, 768),
                                        ("f32", 1, 15000, 256), ("swiglu", 1, 16384, 512), ("f16", 1, 4096, 4096),
-                                       ("swiglu", 4, 6144, 2048)])
+                                       ("swiglu", 4, 6144, 2048), ("swiglu", 8, 4096, 2048), ("resadd", 16, 14400, 1024),
+                                       ("f16", 12, 6144, 4096), ("bias", 5, 4096, 512)])
 def test_narrow_decode_items(dev, epi, M, N, K, narrow, monkeypatch):
     """q4 decode calls the planner would split: 64-column items without a K split (default; half-GPU grids, and small
-    N with short K) and, with P0K_GEMV_NARROW=0, 128-column items in K slices meeting through the workspace; both
-    against the oracle's CPU weight model, ragged last items included."""
+    N with short K; the one-row stream up to 4 rows, k_gemv_mq4 from 5) and, with P0K_GEMV_NARROW=0, 128-column
+    items in K slices meeting through the workspace; both against the oracle's CPU weight model, ragged last items
+    included."""
     monkeypatch.setenv("P0K_GEMV_NARROW", "1" if narrow else "0")
     banner(f"narrow={narrow} {epi} M={M} N={N} K={K}")
     c = make_case(enc="q4g32a.t64", epi=epi, M=M, N=N, K=K, seed=91)
     t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
-    assert t["kernel"] == "gemv" and t["BN"] == (64 if narrow else 128)
+    assert t["kernel"] == ("gemv" if M <= 4 else "gemv_mfma") and t["BN"] == (64 if narrow else 128)
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"{epi} M={M} N={N}")
 
