@@ -274,12 +274,17 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // 256 KB: one item per CU then streams at about 43 GB/s, its ring's bytes in flight over the memory latency;
       // N 4096 / 6144 / 8192 with K 4096: 6.2 / 6.5 / 6.5 against 8.9 / 10.1 / 8.7 us split; N 4096 K 14336: 15.7
       // against 12.0, so long K keeps the split)
+      // (the matrix-core decode kernels, 5..16 q4 rows and q8 / f16 weights, the same with items of one 64-row half)
       const uint32_t tiles128 = (N + 127) / 128;
-      const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u, short_k = (uint64_t)K * 40u <= 256u * 1024u;
-      // (k_gemv_mq4, q4 with 5..16 rows, the same with items of one 64-row half)
-      if (tune.gemv_narrow && (!mf || tune.gemv_mq4) && S >= 2 && we == P0K_ENC_Q4G32A_T64 && (mf || M <= 4) &&
-          epi != P0K_EPI_HEADS && epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) &&
-          K % 256 == 0) {
+      // (q8 / f16 take the filled-grid rule only: N 14336 with one row, q8 K 4096 19.6 against 21.5 us split, f16
+      // K 2048 26.5 against 27.5; with 4 q8 rows 20.1 against 21.8. Their short items are mixed: f16 items of 256 KB,
+      // N 4096 K 2048, 18.8 against 12.7 us at one row (one item per CU, streaming at about 14 GB/s) but 20.0 against
+      // 21.3 at 8 rows and N 6144; so they stay split)
+      const uint32_t kq8 = (we == P0K_ENC_Q8G64S_T64 ? 64u : 32u) * 8u;   // k of one unit in each K-eighth
+      const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u;
+      const bool short_k = we == P0K_ENC_Q4G32A_T64 && (uint64_t)K * 40u <= 256u * 1024u;
+      if (tune.gemv_narrow && S >= 2 && (mf || (we == P0K_ENC_Q4G32A_T64 && M <= 4)) && epi != P0K_EPI_HEADS &&
+          epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) && K % kq8 == 0) {
         narrow = true;
         S = 1;
         KS = K;

@@ -478,11 +478,12 @@ constexpr int MF_KSP = MF_KSM + 8;
 constexpr int MF_XG = 16 * MF_KSP * 2 + 16 * (MF_KSM / 32) * 8;    // X' of 16 rows + (G1, G2) per row and group
 constexpr int MF_LDS = MF_XG + 8 * 64 * 20;                 // + per wave: one q4 unit (64 rows x 16 B) and its scales
 
-template <int WE, int XM>
+// NARROW: items of 64 ws columns with the 8 waves as K-eighths (S = 1, element-wise epilogues), as in k_gemv
+template <int WE, int XM, bool NARROW = false>
 __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
-  constexpr int MT = 16;
+  constexpr int MT = 16, KQ = NARROW ? 2 * GV_KSUB : GV_KSUB, TW = NARROW ? 64 : 128;
   constexpr int UK = MUnit<WE>::UK, PF = MUnit<WE>::PF, KSM = MF_KSP;   // KSM: the X' row stride
-  static_assert(GV_KSUB * MT * 128 * 4 <= MF_LDS, "partials must fit the staging buffer");
+  static_assert(KQ * MT * 128 * 4 <= MF_LDS, "partials must fit the staging buffer");
   __shared__ __attribute__((aligned(16))) uint8_t smem[MF_LDS];
   __shared__ uint32_t sLast;
   f16 *sX = (f16 *)smem;                                       // [MT][KSM] X', pair order of the encoding
@@ -490,10 +491,11 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   float *sR = (float *)smem;                                   // after the stream: partials
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ch = wave / GV_KSUB, sub = wave % GV_KSUB, l16 = lane & 15, kc = lane >> 4;
+  const int ch = NARROW ? 0 : wave / GV_KSUB, sub = NARROW ? wave : wave % GV_KSUB, l16 = lane & 15, kc = lane >> 4;
   const uint32_t tile = blockIdx.x / S, slice = blockIdx.x - tile * S;
-  const uint32_t nB = tile * 128u, kb0 = slice * KS;
-  const uint32_t nuw = KS / UK / GV_KSUB, u0 = sub * nuw;
+  const uint32_t nB = tile * (uint32_t)TW, kb0 = slice * KS;
+  const uint32_t nuw = KS / UK / KQ, u0 = sub * nuw;
+  auto col = [&](uint32_t j) __attribute__((always_inline)) { return NARROW ? j : tile_col(p, (uint32_t)ch, j); };
 
   // q4: lane l loads weight row l of the wave's 64 (16 bytes + its scale word, as the one-row stream does) and the
   // wave regroups the unit through its own LDS slot; q8 / f16: per block, this lane's weight row and the byte offsets
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   uint32_t woff[4], soff[4], rlo[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const uint32_t r = wrow(p, nB + tile_col(p, (uint32_t)ch, WE == W_Q4 ? (uint32_t)lane : (uint32_t)(16 * i + l16)));
+    const uint32_t r = wrow(p, nB + col(WE == W_Q4 ? (uint32_t)lane : (uint32_t)(16 * i + l16)));
     rlo[i] = r & 1u;
     if constexpr (WE == W_Q4) {
       const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 5)) * 1280u;
@@ -692,9 +694,10 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + tile_col(p, (uint32_t)ch, (uint32_t)(16 * i + l16))] = acc[i][r];
+    for (int r = 0; r < 4; r++) sR[(sub * MT + 4 * kc + r) * 128 + col((uint32_t)(16 * i + l16))] = acc[i][r];
   __syncthreads();
-  if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
+  if constexpr (NARROW) finish_fast<MT, KQ, GV_NT, TW>(p, sR, nB, tid);     // (the host sends only S = 1 here)
+  else if (fast_epi(p, S)) finish_fast<MT>(p, sR, nB, tid);
   else finish<MT>(p, sR, part, cnt, S, tile, slice, nB, tid, &sLast);
 }
 
@@ -944,7 +947,11 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
       else hipLaunchKernelGGL((k_gemv_mq4<XM, false>), grid, dim3(MQ_NT), 0, s, p, part, cnt, S, KS);
       return hipGetLastError();
     }
-    if (narrow) return hipErrorInvalidValue;
+    if (narrow) {
+      if (S != 1 || p.epi == E_HEADS || p.epi == E_ONORMGATE) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((k_gemv_mf<WE, XM, true>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
   }
@@ -971,7 +978,7 @@ hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *c
                        hipStream_t s, bool mf, bool mq4, bool mx, bool narrow) {
   const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
-  if (narrow && (we != W_Q4 || S != 1 || (mf && !mq4))) return hipErrorInvalidValue;
+  if (narrow && (S != 1 || KS % (2 * quant) || (!mf && we != W_Q4))) return hipErrorInvalidValue;
   switch (we) {
   case W_Q4: return launch1<W_Q4>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);
   case W_Q8: return launch1<W_Q8>(p, xm, part, cnt, S, KS, s, mf, mq4, mx, narrow);

@@ -222,6 +222,29 @@ def test_narrow_decode_items(dev, epi, M, N, K, narrow, monkeypatch):
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"{epi} M={M} N={N}")
 
 
+@pytest.mark.parametrize("narrow", [True, False])
+@pytest.mark.parametrize("enc,epi,M,N,K,mq4", [("q8g64s.t64", "f16", 1, 14336, 4096, "1"),
+                                               ("q8g64s.t64", "swiglu", 3, 14400, 1024, "1"),
+                                               ("q8g64s.t64", "resadd", 16, 14400, 2048, "1"),
+                                               ("f16", "bias", 2, 14336, 2048, "1"), ("f16", "swiglu", 9, 14400, 512, "1"),
+                                               ("f16", "f32", 1, 16000, 256, "1"),
+                                               ("q4g32a.t64", "swiglu", 8, 4096, 2048, "0"),
+                                               ("q4g32a.t64", "f16", 16, 6160, 4096, "0")])
+def test_narrow_matrix_core_decode(dev, enc, epi, M, N, K, mq4, narrow, monkeypatch):
+    """the matrix-core decode (q8 and f16 weights; q4 with X' staged in LDS under P0K_GEMV_MQ4=0) in 64-column items
+    with the 8 waves as K-eighths, against its 128-column items in K slices (P0K_GEMV_NARROW=0): both against the
+    oracle's CPU weight model, ragged last items and unaligned N included."""
+    monkeypatch.setenv("P0K_GEMV_NARROW", "1" if narrow else "0")
+    monkeypatch.setenv("P0K_GEMV_MQ4", mq4)
+    banner(f"narrow={narrow} {enc} {epi} M={M} N={N} K={K} mq4={mq4}")
+    c = make_case(enc=enc, epi=epi, M=M, N=N, K=K, seed=93)
+    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    assert t["kernel"] == "gemv_mfma" and t["BN"] == (64 if narrow else 128)
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16,
+                 what=f"{enc} {epi} M={M} N={N} K={K}")
+
+
 # ------------------------------------------------------------------------------------------------ dequantisation
 def _adversarial_q4(rows, K, seed):
     """random codes with (scale, min) words that include far-apart exponents (the decoder's exact-fp32 path)."""
