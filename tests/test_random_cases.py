@@ -99,3 +99,51 @@ def test_random_glu_case_matches_oracle(dev, kw):
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on {kern}")
+
+
+def _narrow_cases(n=16, seed=20251204):
+    """decode calls wide enough for 64-column items without a K split (at least 14336 ws columns: the 128-column
+    tiles would fill only half of the CUs), every weight encoding and 1..16 rows, with the argument offsets of the
+    sweep above (x.ld / x.k0, y.n0, wk0, wr0) and ragged N"""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        enc = ["q4g32a.t64", "q8g64s.t64", "f16"][rng.integers(3)]
+        M = int([1, 2, 3, 4, 5, 8, 13, 16][rng.integers(8)])
+        if enc == "q4g32a.t64" and M <= 4:
+            M = 5 + int(rng.integers(0, 12))       # (1..4 q4 rows: the stream kernel, covered elsewhere)
+        epi = ["f16", "f32", "resadd", "bias", "swiglu"][rng.integers(5)]
+        K = int(512 * rng.integers(1, 5))
+        kw = dict(enc=enc, xmode=["f16", "f16", "rms"][rng.integers(3)], epi=epi, M=M, K=K,
+                  N=14336 + 8 * int(rng.integers(0, 200)), seed=int(rng.integers(1, 1 << 20)))
+        if epi == "swiglu":
+            kw.update(act=["silu", "gelu"][rng.integers(2)], bias=bool(rng.integers(2)))
+        if epi == "resadd":
+            kw.update(gate=bool(rng.integers(2)), bias=bool(rng.integers(2)), store=bool(rng.integers(2)))
+        if epi == "bias":
+            kw.update(res=bool(rng.integers(2)))
+        if rng.integers(2):
+            kw.update(ld_pad=int(4 * rng.integers(0, 5)), k0=int(4 * rng.integers(0, 9)))
+        if rng.integers(2):
+            kw.update(n0=int(8 * rng.integers(0, 3)))
+        if rng.integers(3) == 0:
+            kw.update(wk0=(64 if enc == "q8g64s.t64" else 32) * int(rng.integers(1, 3)))
+        if epi != "swiglu" and rng.integers(4) == 0:
+            kw.update(wr0=64)
+        out.append(kw)
+    return out
+
+
+NARROW_CASES = _narrow_cases()
+
+
+@pytest.mark.parametrize("kw", NARROW_CASES, ids=[f"{i:02d}-{k['enc'][:2]}-{k['epi']}-M{k['M']}-N{k['N']}-K{k['K']}"
+                                                  for i, k in enumerate(NARROW_CASES)])
+def test_random_narrow_case_matches_oracle(dev, kw):
+    c = make_case(**kw)
+    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    assert t["kernel"] == "gemv_mfma" and t["BN"] == 64, t
+    print(f"[p0k-test] random narrow case {kw}", flush=True)
+    got = c.run_device(dev)
+    want = c.run_oracle()
+    assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on 64-column items")
