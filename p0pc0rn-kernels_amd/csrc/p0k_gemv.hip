@@ -28,6 +28,8 @@
 #include "p0k_device.h"
 #include "p0k_launch.h"
 
+#include <type_traits>
+
 namespace p0k {
 
 #ifndef P0K_GV_KSUB
@@ -715,25 +717,24 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 //     1024 + 16 q high), and the same swaps broadcast row 16 i + l16's (scale, min) word to it
 //   * each lane reads its A fragment, X' row l16 (rows past M repeat row M - 1, whose products land in output rows
 //     that are never stored), k = 8 kc .. 8 kc + 7 of the unit, and puts it into the pair order of the decode, the
-//     high-nibble positions scaled by 1/16. fp16 X with 16-byte rows (XL): the item's X rows are copied to LDS as
-//     they are by the load-to-LDS path (global_load_lds_dwordx4, no registers), issued before the weight ring so the
-//     copy runs under the ring's first HBM latency; rows 16 bytes longer than K, so the 16 rows one A read touches
-//     start in different banks. Otherwise (rms / lnmod prologues, unaligned X) the fragment is computed from X with
+//     high-nibble positions scaled by 1/16. fp16 X with 16-byte rows (XL): each unit's 16 X rows x 32 k (1 KB) are
+//     copied to the wave's LDS slot of its ring entry by one load-to-LDS instruction (global_load_lds_dwordx4, no
+//     registers) issued with the unit's weight loads, so X streams with the weights instead of being staged whole
+//     before them (16 rows x 4096 k: 128 KB per item, 18.7-19.1 against 19.8-19.9 us at M = 16). Otherwise (rms / lnmod prologues, unaligned X) the fragment is computed from X with
 //     the same unit's loads.
 //   * two MFMAs against constant B operands give, for every output column, -G1 = -(1024 X_lo + 64 X_hi) and
 //     G2 = X_lo + X_hi of the unit's rows; each block's MFMA starts from -G1, so it returns sum x q directly, and
 //     y += s (sum x q) + mn G2 in registers (the fp32 weight model of the stream above).
 // (12 or 16 waves per item, or 2 or 4 units in flight per wave, measured slower)
 constexpr int MQ_KQ = 8, MQ_NT = 64 * MQ_KQ, MQ_PF = 3;     // waves = K parts of an item; units in flight per wave
-constexpr int MQ_XP = MF_KSM * 2 + 16;                       // LDS bytes per staged X row
-constexpr int MQ_LDS = 16 * MQ_XP > MQ_KQ * 16 * 128 * 4 ? 16 * MQ_XP : MQ_KQ * 16 * 128 * 4;
 // NARROW: items of 64 ws columns (one half: 4 blocks of 16 rows), S = 1 and the element-wise epilogues only, for calls
 // whose 128-column items the planner would split (the same rule as the one-row stream's 64-column items)
 template <int XM, bool XL, bool NARROW = false>
 __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
   constexpr int MT = 16, PF = MQ_PF, NH = NARROW ? 1 : 2, TW = 64 * NH;   // halves (64-row blocks) per item
   static_assert(!XL || XM == X_F16, "X rows are copied as they are only without a prologue");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[XL ? MQ_LDS : MQ_KQ * MT * 128 * 4];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[MQ_KQ * MT * 128 * 4];
+  static_assert(MQ_KQ * MQ_PF * 1024 <= MQ_KQ * MT * 128 * 4, "X unit slots fit the partials' buffer");
   __shared__ uint32_t sLast;
   float *sR = (float *)smem;                                   // after the stream: the K-eighths' partials
 
@@ -756,25 +757,24 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   const uint32_t xrow = (uint32_t)l16 < p.M ? (uint32_t)l16 : p.M - 1u;
   const uint32_t xk0 = kb0 + u0 * 32u + (uint32_t)kc * 8u;
 
-  if constexpr (XL) {
-    // X rows [0, min(M, 16)) of the slice -> LDS, 1 KB per instruction (lane l: 16 bytes at 16 l), instruction q of
-    // the list taken by wave q % 8
-    // (a row's last instruction may reach past KS: those lanes re-read the row's first 16 bytes into the row's
-    // padding, which an LDS row of whole KB plus 16 bytes leaves room for)
-    const uint32_t mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT, cpr = (KS + 511u) / 512u, nq = mr * cpr;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)smem;
-    for (uint32_t q = (uint32_t)wave; q < nq; q += (uint32_t)MQ_KQ) {
-      const uint32_t m = q / cpr, c = q - m * cpr, k = c * 512u + 8u * (uint32_t)lane;
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + m * (uint32_t)MQ_XP + c * 1024u);
-      const uint8_t *src = p.X + ((size_t)m * p.ldx + p.kx0 + kb0 + (k < KS ? k : 0u)) * 2u;
-      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
-    }
-  }
+  // XL: the unit's X' block (16 rows x 32 k, 1 KB) goes to this wave's LDS slot for the ring entry by one load-to-LDS
+  // instruction issued with the unit's weight loads (before them, so it has landed once they have): lane l copies row
+  // l / 4, 16-byte chunk (l % 4) ^ ((l / 16) % 4) of it (rows past M repeat row M - 1); the chunk swizzle makes the
+  // A reads (lane (kc, l16): row l16, chunk kc) conflict-free
+  const uint32_t xslot0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)smem + (uint32_t)wave * (MQ_PF * 1024u);
+  const uint32_t xcr = (uint32_t)lane >> 2 < p.M ? (uint32_t)lane >> 2 : p.M - 1u, xcc = ((uint32_t)lane & 3u) ^ (((uint32_t)lane >> 4) & 3u);
+  const uint8_t *xcp = p.X + ((size_t)xcr * p.ldx + p.kx0 + kb0 + u0 * 32u + xcc * 8u) * 2u;
+  const uint32_t xrd = (uint32_t)wave * (MQ_PF * 1024u) + (4u * (uint32_t)l16 + ((uint32_t)kc ^ (((uint32_t)l16 >> 2) & 3u))) * 16u;
 
   struct U { u32x4 code[NH]; uint32_t sm[NH]; u32x4 x; };
   const srsrc wr = stream_rsrc(p.W);
-  auto load = [&](U &u, uint32_t j) __attribute__((always_inline)) {
+  auto load = [&](U &u, uint32_t j, int slot) __attribute__((always_inline)) {
     const uint32_t du = j * 1280u;
+    if constexpr (XL) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(xslot0 + (uint32_t)slot * 1024u);
+      const uint8_t *src = xcp + j * 64u;
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
+    }
 #pragma unroll
     for (int h = 0; h < NH; h++) u.code[h] = sload128(wr, woff[h] + du);
 #pragma unroll
@@ -782,9 +782,8 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
     if constexpr (!XL) u.x = xload8<XM>(p, xrow, RowCtx{0, 0, 0}, xk0 + j * 32u);
   };
   // the A fragment of the wave's unit j
-  const uint8_t *xs = smem + xrow * (uint32_t)MQ_XP + (u0 * 32u + (uint32_t)kc * 8u) * 2u;
-  auto xfrag = [&](const U &u, uint32_t j) __attribute__((always_inline)) -> u32x4 {
-    if constexpr (XL) return *(const u32x4 *)(xs + j * 64u);
+  auto xfrag = [&](const U &u, int slot) __attribute__((always_inline)) -> u32x4 {
+    if constexpr (XL) return *(const u32x4 *)(smem + xrd + (uint32_t)slot * 1024u);
     else return u.x;
   };
 
@@ -800,8 +799,11 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
 #pragma unroll
   for (int i = 0; i < 4 * NH; i++) acc[i] = z4;
 
-  auto compute = [&](const U &u, uint32_t j) __attribute__((always_inline)) {
-    u32x4 xv = xperm<W_Q4>(xfrag(u, j));
+  // XL: before the unit's X' read, wait for its copy: W loads were issued after it (own weights, then the other
+  // entries of the ring), and loads complete in order
+  auto compute = [&](const U &u, int slot, auto W) __attribute__((always_inline)) {
+    if constexpr (XL) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(decltype(W)::value) : "memory");
+    u32x4 xv = xperm<W_Q4>(xfrag(u, slot));
     xv.y = as_u(as_h2(xv.y) * r16);
     xv.w = as_u(as_h2(xv.w) * r16);
     const f16x8 a = __builtin_bit_cast(f16x8, xv);
@@ -844,30 +846,31 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   U ring[PF];
 #pragma unroll
   for (int j = 0; j < PF; j++) {
-    load(ring[j], (uint32_t)j < nl ? (uint32_t)j : nl);
+    load(ring[j], (uint32_t)j < nl ? (uint32_t)j : nl, j);
     __builtin_amdgcn_sched_barrier(0);
-  }
-  if constexpr (XL) {
-    // the X copy is older than the ring's loads (loads complete in order): wait for it alone, then for every wave's
-    constexpr int LPU = 2 * NH;                                // loads per unit
-    __builtin_amdgcn_s_waitcnt((LPU * PF & 15) | (((LPU * PF) >> 4) << 14) | 0x0f70);   // vmcnt(LPU PF)
-    __syncthreads();
   }
   uint32_t j0 = 0;
 #pragma unroll 1
   for (; j0 + PF <= nuw; j0 += PF) {
+    constexpr int LPU = 2 * NH;                                // weight loads per unit
 #pragma unroll
     for (int j = 0; j < PF; j++) {
-      compute(ring[j], j0 + j);
+      compute(ring[j], j, std::integral_constant<int, LPU + (PF - 1) * (LPU + 1)>{});
       const uint32_t nx = j0 + PF + j;
-      load(ring[j], nx < nuw ? nx : nl);
+      load(ring[j], nx < nuw ? nx : nl, j);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-#pragma unroll
-  for (int j = 0; j < PF; j++)
-    if (j0 + j < nuw) compute(ring[j], j0 + j);
-  if constexpr (XL) __syncthreads();                           // X' is dead: the buffer takes the partials
+  // (the tail issues no loads: fewer are younger than each unit's copy)
+  constexpr int LPU = 2 * NH;
+  if (j0 < nuw) compute(ring[0], 0, std::integral_constant<int, LPU + (PF - 1) * (LPU + 1)>{});
+  static_assert(PF == 3, "the tail below is written for 3 units in flight");
+  if (j0 + 1 < nuw) compute(ring[1], 1, std::integral_constant<int, LPU + (PF - 2) * (LPU + 1)>{});
+  if (j0 + 2 < nuw) compute(ring[2], 2, std::integral_constant<int, LPU>{});
+  if constexpr (XL) {                                          // the X' slots are dead: the buffer takes the partials
+    __builtin_amdgcn_s_waitcnt(0x0f70);                        // vmcnt(0): no copy may land after this
+    __syncthreads();
+  }
 
   // D[m = 4 kc + r][row 16 i + l16] of the tile's rows 64 h + ...; the K-eighths meet in LDS
 #pragma unroll
