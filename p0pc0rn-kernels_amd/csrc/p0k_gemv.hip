@@ -725,8 +725,12 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 //   * two MFMAs against constant B operands give, for every output column, -G1 = -(1024 X_lo + 64 X_hi) and
 //     G2 = X_lo + X_hi of the unit's rows; each block's MFMA starts from -G1, so it returns sum x q directly, and
 //     y += s (sum x q) + mn G2 in registers (the fp32 weight model of the stream above).
-// (12 or 16 waves per item, or 2 or 4 units in flight per wave, measured slower)
-constexpr int MQ_KQ = 8, MQ_NT = 64 * MQ_KQ, MQ_PF = 3;     // waves = K parts of an item; units in flight per wave
+// (12 or 16 waves per item measured slower; with X streamed per unit, 2 units in flight per wave beat 1, 3 and 4:
+// M = 16 17.7-18.1 against 18.3-18.4 / 18.2-18.5 / 19.8-19.9 us, M = 8 16.8-17.2 against 17.9 / 17.3-17.8 / 18.4)
+#ifndef P0K_MQ_PF
+#define P0K_MQ_PF 2
+#endif
+constexpr int MQ_KQ = 8, MQ_NT = 64 * MQ_KQ, MQ_PF = P0K_MQ_PF;     // waves = K parts of an item; units in flight per wave
 // NARROW: items of 64 ws columns (one half: 4 blocks of 16 rows), S = 1 and the element-wise epilogues only, for calls
 // whose 128-column items the planner would split (the same rule as the one-row stream's 64-column items)
 template <int XM, bool XL, bool NARROW = false>
@@ -863,10 +867,16 @@ __global__ __launch_bounds__(MQ_NT) void k_gemv_mq4(Params p, float *part, uint3
   }
   // (the tail issues no loads: fewer are younger than each unit's copy)
   constexpr int LPU = 2 * NH;
-  if (j0 < nuw) compute(ring[0], 0, std::integral_constant<int, LPU + (PF - 1) * (LPU + 1)>{});
-  static_assert(PF == 3, "the tail below is written for 3 units in flight");
-  if (j0 + 1 < nuw) compute(ring[1], 1, std::integral_constant<int, LPU + (PF - 2) * (LPU + 1)>{});
-  if (j0 + 2 < nuw) compute(ring[2], 2, std::integral_constant<int, LPU>{});
+  static_assert(PF >= 1 && PF <= 4, "the tail below covers 1..4 units in flight");
+  auto tail = [&](auto J) __attribute__((always_inline)) {
+    constexpr int j = decltype(J)::value;
+    if constexpr (j < PF)
+      if (j0 + j < nuw) compute(ring[j], j, std::integral_constant<int, LPU + (PF - 1 - j) * (LPU + 1)>{});
+  };
+  tail(std::integral_constant<int, 0>{});
+  tail(std::integral_constant<int, 1>{});
+  tail(std::integral_constant<int, 2>{});
+  tail(std::integral_constant<int, 3>{});
   if constexpr (XL) {                                          // the X' slots are dead: the buffer takes the partials
     __builtin_amdgcn_s_waitcnt(0x0f70);                        // vmcnt(0): no copy may land after this
     __syncthreads();
