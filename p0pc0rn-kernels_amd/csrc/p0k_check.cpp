@@ -276,7 +276,8 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // against 12.0, so long K keeps the split)
       // (the matrix-core decode kernels, 5..16 q4 rows and q8 / f16 weights, the same with items of one 64-row half)
       const uint32_t tiles128 = (N + 127) / 128;
-      // (q8 / f16 take the filled-grid rule only: N 14336 with one row, q8 K 4096 19.6 against 21.5 us split, f16
+      // (q8 / f16 take the filled-grid rule only: N 14336 with one row, q8 K 4096 19.6 against 21.5 us split (with
+      // the earlier 8-byte q8 loads), f16
       // K 2048 26.5 against 27.5; with 4 q8 rows 20.1 against 21.8. Their short items are mixed: f16 items of 256 KB,
       // N 4096 K 2048, 18.8 against 12.7 us at one row (one item per CU, streaming at about 14 GB/s) but 20.0 against
       // 21.3 at 8 rows and N 6144; so they stay split)

@@ -469,7 +469,7 @@ struct MUnit;
 template <>
 struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 4; u32x4 code; uint32_t sm; };   // row `lane`, as loaded
 template <>
-struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x2 code[4][2]; uint32_t s[4]; };
+struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x4 code[4]; uint32_t s[4]; };
 template <>
 struct MUnit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
 
@@ -514,7 +514,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       soff[i] = rec + 1024u + (r & 63u) * 4u;
     } else if constexpr (WE == W_Q8) {
       const uint32_t rec = ((r >> 6) * p.wG + ((p.wk0 + kb0) >> 6)) * 4224u;
-      woff[i] = rec + (r & 63u) * 64u + kc * 8u;
+      woff[i] = rec + (r & 63u) * 64u + kc * 16u;
       soff[i] = rec + 4096u + (r & 62u) * 2u;
     } else {
       woff[i] = (r * p.wG + p.wk0 + kb0) * 2u + kc * 16u;
@@ -533,8 +533,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       if constexpr (WE == W_Q8) {
-        u.code[i][0] = sload64(wr, woff[i] + du);
-        u.code[i][1] = sload64(wr, woff[i] + du + 32u);
+        u.code[i] = sload128(wr, woff[i] + du);
         u.s[i] = sload32(wr, soff[i] + du);
       } else {
         u.v[i] = sload128(wr, woff[i] + du);
@@ -589,7 +588,9 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       }
 #pragma unroll
       for (int h = 0; h < UK / 32; h++) {
-        const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + h * 32 + kc * 8) & amask);
+        // q8: lane kc holds k 16 kc .. 16 kc + 15 of the unit (one 16-byte load per row), 8 of them per MFMA
+        const int ka = WE == W_Q8 ? 16 * kc + 8 * h : 32 * h + 8 * kc;
+        const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + ka) & amask);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           u32x4 bw;
@@ -597,7 +598,7 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
             const uint32_t w = qw[i], w8 = w >> 8;
             bw = (u32x4){(w & mlo) | mag, (w & mhi) | mag, (w8 & mlo) | mag, (w8 & mhi) | mag};
           } else {
-            const uint32_t x0 = u.code[i][h].x ^ 0x80808080u, x1 = u.code[i][h].y ^ 0x80808080u;
+            const uint32_t x0 = (h ? u.code[i].z : u.code[i].x) ^ 0x80808080u, x1 = (h ? u.code[i].w : u.code[i].y) ^ 0x80808080u;
             bw = (u32x4){perm(m64, x0, 0x04020400u), perm(m64, x0, 0x04030401u), perm(m64, x1, 0x04020400u),
                          perm(m64, x1, 0x04030401u)};
           }
