@@ -281,7 +281,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // K 2048 26.5 against 27.5; with 4 q8 rows 20.1 against 21.8. Their short items are mixed: f16 items of 256 KB,
       // N 4096 K 2048, 18.8 against 12.7 us at one row (one item per CU, streaming at about 14 GB/s) but 20.0 against
       // 21.3 at 8 rows and N 6144; so they stay split)
-      const uint32_t kq8 = (we == P0K_ENC_Q8G64S_T64 ? 64u : 32u) * 8u;   // k of one unit in each K-eighth
+      const uint32_t kq8 = gemv_unit_k(we, mf) * 8u;   // k of one unit in each K-eighth
       const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u;
       const bool short_k = we == P0K_ENC_Q4G32A_T64 && (uint64_t)K * 40u <= 256u * 1024u;
       if (tune.gemv_narrow && S >= 2 && (mf || (we == P0K_ENC_Q4G32A_T64 && M <= 4)) && epi != P0K_EPI_HEADS &&
@@ -293,7 +293,7 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // tuning override of the slice count (P0K_GEMV_SLICES=n), honoured only when it keeps whole units per wave
       if (tune.gemv_slices) {
         narrow = false;
-        unsigned s2 = tune.gemv_slices, quant = we == P0K_ENC_Q8G64S_T64 ? 256u : 128u;
+        unsigned s2 = tune.gemv_slices, quant = gemv_unit_k(we, mf) * 4u;
         if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;

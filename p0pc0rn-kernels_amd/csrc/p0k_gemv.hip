@@ -471,7 +471,7 @@ struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 4; u32x4 code; uint32_t 
 template <>
 struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x4 code[4]; uint32_t s[4]; };
 template <>
-struct MUnit<W_F16> { static constexpr int UK = 32, PF = 4; u32x4 v[4]; };
+struct MUnit<W_F16> { static constexpr int UK = 64, PF = 2; u32x4 v[4][2]; };   // lane: 16 k (32 B) of a row
 
 constexpr int MF_KSM = 4096;                                // longest K slice of one item
 // X' rows are MF_KSM + 8 halfs apart: the 16 rows an MFMA A read touches then start 4 banks apart instead of all in
@@ -517,11 +517,11 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       woff[i] = rec + (r & 63u) * 64u + kc * 16u;
       soff[i] = rec + 4096u + (r & 62u) * 2u;
     } else {
-      woff[i] = (r * p.wG + p.wk0 + kb0) * 2u + kc * 16u;
+      woff[i] = (r * p.wG + p.wk0 + kb0) * 2u + kc * 32u;
       soff[i] = 0u;
     }
   }
-  constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 64u;
+  constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 128u;
 
   const srsrc wr = stream_rsrc(p.W);
   auto load = [&](MUnit<WE> &u, uint32_t unit) {
@@ -535,8 +535,9 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
       if constexpr (WE == W_Q8) {
         u.code[i] = sload128(wr, woff[i] + du);
         u.s[i] = sload32(wr, soff[i] + du);
-      } else {
-        u.v[i] = sload128(wr, woff[i] + du);
+      } else {                                                 // (two loads: 16 whole 128-byte row pieces)
+        u.v[i][0] = sload128(wr, woff[i] + du);
+        u.v[i][1] = sload128(wr, woff[i] + du + 16u);
       }
     }
     }
@@ -555,11 +556,13 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
 
   auto compute = [&](const MUnit<WE> &u, uint32_t unit) {
     if constexpr (WE == W_F16) {
-      const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + kc * 8) & amask);
+      // lane kc holds k 16 kc .. 16 kc + 15 of the unit, 8 of them per MFMA
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const f16x8 b = __builtin_bit_cast(f16x8, u.v[i]);
-        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[i], 0, 0, 0);
+      for (int h = 0; h < 2; h++) {
+        const f16x8 a = __builtin_bit_cast(f16x8, *(const u32x4 *)(sX + l16 * KSM + unit * UK + 16 * kc + 8 * h) & amask);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, u.v[i][h]), acc[i], 0, 0, 0);
       }
     } else {
       // (G1, G2) of rows m = 4 kc + r for this unit
@@ -913,12 +916,14 @@ static uint32_t ks_max_of(uint32_t M, int we, bool mf, bool mx) {
   return stream_ksm<16>(we);
 }
 unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx) { return ks_max_of(M, we, mf, mx); }
+// k of one weight unit: q8 64 (a record), f16 on the matrix cores 64 (one 128-byte row piece), else 32
+unsigned gemv_unit_k(int we, bool mf) { return we == W_Q8 || (we == W_F16 && mf) ? 64u : 32u; }
 
 // Slices per tile: the fewest that fill the GPU with items (about one per CU) and keep each slice's X' inside the LDS
 // budget, with a whole number of units per K-quarter.
 void gemv_split(const Params &p, int we, unsigned cus, bool mf, bool mx, unsigned *S_out, unsigned *KS_out) {
   const uint32_t tiles = (p.N + 127) / 128;
-  const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;     // k per "one unit in each K-quarter"
+  const uint32_t quant = gemv_unit_k(we, mf) * GV_KSUB;     // k per "one unit in each K-quarter"
   const uint32_t ksm = ks_max_of(p.M, we, mf, mx);
   uint32_t S = 1;
   while ((tiles * S < cus * 7u / 8u || p.K / S > ksm) && p.K % (2u * S * quant) == 0) S *= 2u;
@@ -990,7 +995,7 @@ static hipError_t launch1(const Params &p, int xm, float *part, uint32_t *cnt, u
 
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, uint32_t *cnt, uint32_t S, uint32_t KS,
                        hipStream_t s, bool mf, bool mq4, bool mx, bool narrow) {
-  const uint32_t quant = (we == W_Q8 ? 64u : 32u) * GV_KSUB;
+  const uint32_t quant = gemv_unit_k(we, mf) * GV_KSUB;
   if (p.M > (uint32_t)GEMV_MAX_M || S == 0 || KS * S != p.K || KS % quant) return hipErrorInvalidValue;
   if (narrow && (S != 1 || KS % (2 * quant) || (!mf && we != W_Q4))) return hipErrorInvalidValue;
   switch (we) {

@@ -32,6 +32,7 @@ hipError_t launch_gemm_dma(const Params &p, int we, int xg, unsigned bm, unsigne
 // narrow: the stream kernel (q4, M <= 4, S = 1, element-wise epilogues) over items of 64 columns instead of 128
 void gemv_split(const Params &p, int we, unsigned cus, bool mf, bool mx, unsigned *S, unsigned *KS);
 unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx);   // longest K slice one item stages
+unsigned gemv_unit_k(int we, bool mf);                      // k of one decode weight unit
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s,
                        bool mf, bool mq4, bool mx, bool narrow);
 // rowstats (src/ops/misc.js:16-44)

@@ -227,7 +227,7 @@ def test_narrow_decode_items(dev, epi, M, N, K, narrow, monkeypatch):
                                                ("q8g64s.t64", "swiglu", 3, 14400, 1024, "1"),
                                                ("q8g64s.t64", "resadd", 16, 14400, 2048, "1"),
                                                ("f16", "bias", 2, 14336, 2048, "1"), ("f16", "swiglu", 9, 14400, 512, "1"),
-                                               ("f16", "f32", 1, 16000, 256, "1"),
+                                               ("f16", "f32", 1, 16000, 512, "1"),
                                                ("q4g32a.t64", "swiglu", 8, 4096, 2048, "0"),
                                                ("q4g32a.t64", "f16", 16, 6160, 4096, "0")])
 def test_narrow_matrix_core_decode(dev, enc, epi, M, N, K, mq4, narrow, monkeypatch):
