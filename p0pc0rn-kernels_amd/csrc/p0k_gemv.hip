@@ -469,10 +469,12 @@ struct MUnit;
 template <>
 struct MUnit<W_Q4> { static constexpr int UK = 32, PF = 4; u32x4 code; uint32_t sm; };   // row `lane`, as loaded
 template <>
-struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 4; u32x4 code[4]; uint32_t s[4]; };
+struct MUnit<W_Q8> { static constexpr int UK = 64, PF = 3; u32x4 code[4]; uint32_t s[4]; };
 template <>
-struct MUnit<W_F16> { static constexpr int UK = 64, PF = 2; u32x4 v[4][2]; };   // lane: 16 k (32 B) of a row
+struct MUnit<W_F16> { static constexpr int UK = 64, PF = 3; u32x4 v[4][2]; };   // lane: 16 k (32 B) of a row
 
+// (units in flight per wave, q8 / f16: 3; q8 with 2 / 4 / 6: 14.3 / 14.9 / 27.3 against 13.4 us at N 14336, K 4096,
+// M = 1; f16 with 2 / 4: 23.8 / 34.1 against 22.7 us at N 14336, K 2048, M = 1, 11.3 / 13.6 against 11.5 at N 4096)
 constexpr int MF_KSM = 4096;                                // longest K slice of one item
 // X' rows are MF_KSM + 8 halfs apart: the 16 rows an MFMA A read touches then start 4 banks apart instead of all in
 // one bank (8 KB rows)
