@@ -483,10 +483,15 @@ constexpr int MF_XG = 16 * MF_KSP * 2 + 16 * (MF_KSM / 32) * 8;    // X' of 16 r
 constexpr int MF_LDS = MF_XG + 8 * 64 * 20;                 // + per wave: one q4 unit (64 rows x 16 B) and its scales
 
 // NARROW: items of 64 ws columns with the 8 waves as K-eighths (S = 1, element-wise epilogues), as in k_gemv
-template <int WE, int XM, bool NARROW = false>
+// XS (q8 / f16 with fp16 X of 16-byte rows): no X' staging; each unit's 16 X rows x 64 k (2 KB) are copied into the
+// wave's LDS slot of its ring entry by two load-to-LDS instructions issued with the unit's weight loads, and q8's G1
+// comes from two MFMAs against a constant B operand, as in k_gemv_mq4
+template <int WE, int XM, bool NARROW = false, bool XS = false>
 __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32_t *cnt, uint32_t S, uint32_t KS) {
   constexpr int MT = 16, KQ = NARROW ? 2 * GV_KSUB : GV_KSUB, TW = NARROW ? 64 : 128;
   constexpr int UK = MUnit<WE>::UK, PF = MUnit<WE>::PF, KSM = MF_KSP;   // KSM: the X' row stride
+  static_assert(!XS || (WE != W_Q4 && XM == X_F16 && UK == 64), "streamed X: q8 / f16 units of 64 k, fp16 X");
+  static_assert(GV_NT / 64 * PF * 2048 <= MF_LDS, "X unit slots fit the staging buffer");
   static_assert(KQ * MT * 128 * 4 <= MF_LDS, "partials must fit the staging buffer");
   __shared__ __attribute__((aligned(16))) uint8_t smem[MF_LDS];
   __shared__ uint32_t sLast;
@@ -526,8 +531,21 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : WE == W_Q8 ? 4224u : 128u;
 
   const srsrc wr = stream_rsrc(p.W);
-  auto load = [&](MUnit<WE> &u, uint32_t unit) {
+  // XS: lane l copies row l / 4 (rows past M repeat row M - 1, whose outputs are never stored), 16-byte chunk
+  // (l % 4) ^ ((l / 16) % 4) of each 32-k half of the unit; slot: [half][row][chunk] (1 KB halves)
+  const uint32_t xslot0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)smem + (uint32_t)wave * (PF * 2048u);
+  const uint32_t xcr = (uint32_t)lane >> 2 < p.M ? (uint32_t)lane >> 2 : p.M - 1u, xcc = ((uint32_t)lane & 3u) ^ (((uint32_t)lane >> 4) & 3u);
+  const uint8_t *xcp = p.X + ((size_t)xcr * p.ldx + p.kx0 + kb0 + xcc * 8u) * 2u;
+  auto load = [&](MUnit<WE> &u, uint32_t unit, int slot = 0) {
     const uint32_t du = unit * USTRIDE;
+    if constexpr (XS) {
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(xslot0 + (uint32_t)slot * 2048u + (uint32_t)hh * 1024u);
+        const uint8_t *src = xcp + (unit * 64u + (uint32_t)hh * 32u) * 2u;
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory");
+      }
+    }
     if constexpr (WE == W_Q4) {
       u.code = sload128(wr, woff[0] + du);
       u.sm = sload32(wr, soff[0] + du);
@@ -555,6 +573,46 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
   // A rows past M are not staged: the lanes of those rows AND their (unwritten) LDS words with 0
   const uint32_t am = l16 < (int)p.M ? 0xffffffffu : 0u;
   const u32x4 amask = (u32x4){am, am, am, am};
+
+  // XS: the A fragments of the unit in the slot (lane (kc, l16), MFMA h: X row l16, k = 16 kc + 8 h .. + 7, i.e. half
+  // kc / 2, chunk 2 (kc % 2) + h), after its copy has landed (W loads were issued after it; loads complete in order)
+  auto compute_xs = [&](const MUnit<WE> &u, int slot, auto W) __attribute__((always_inline)) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(decltype(W)::value) : "memory");
+    f16x8 a[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t c = 2u * ((uint32_t)kc & 1u) + (uint32_t)h;
+      const u32x4 raw = *(const u32x4 *)(smem + (uint32_t)wave * (PF * 2048u) + (uint32_t)slot * 2048u +
+                                         ((uint32_t)kc >> 1) * 1024u + (4u * (uint32_t)l16 + (c ^ (((uint32_t)l16 >> 2) & 3u))) * 16u);
+      a[h] = __builtin_bit_cast(f16x8, xperm<WE>(raw));
+    }
+    if constexpr (WE == W_F16) {
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h], __builtin_bit_cast(f16x8, u.v[i][h]), acc[i], 0, 0, 0);
+    } else if constexpr (WE == W_Q8) {
+      // -G1 = -1152 (sum of the unit's x) in every column, from a constant B of -1152
+      const f16x8 bneg = __builtin_bit_cast(f16x8, (u32x4){0xE480E480u, 0xE480E480u, 0xE480E480u, 0xE480E480u});
+      f32x4 ng1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bneg, (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      ng1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bneg, ng1, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        f32x4 d = ng1;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t x0 = (h ? u.code[i].z : u.code[i].x) ^ 0x80808080u, x1 = (h ? u.code[i].w : u.code[i].y) ^ 0x80808080u;
+          const u32x4 bw = (u32x4){perm(m64, x0, 0x04020400u), perm(m64, x0, 0x04030401u), perm(m64, x1, 0x04020400u),
+                                   perm(m64, x1, 0x04030401u)};
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h], __builtin_bit_cast(f16x8, bw), d, 0, 0, 0);
+        }
+        const float sc = (float)__builtin_bit_cast(f16, (uint16_t)(rlo[i] ? (u.s[i] >> 16) : (u.s[i] & 0xffffu)));
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][r] = fmaf(sc, d[r], acc[i][r]);
+      }
+    }
+  };
 
   auto compute = [&](const MUnit<WE> &u, uint32_t unit) {
     if constexpr (WE == W_F16) {
@@ -625,78 +683,115 @@ __global__ __launch_bounds__(GV_NT) void k_gemv_mf(Params p, float *part, uint32
     }
   };
 
-  // X' of the slice for the rows < M only (the MFMA A reads of rows past M take zeros instead); one thread per
-  // (row, unit) task stages the unit's chunks and (q4 / q8) its sums of the unscaled X' over the low / high positions
-  // -> (G1, G2); q4: the high-nibble positions (odd pair slots) are stored as x / 16. The chunks of the first XT
-  // tasks of every thread (all of them for K <= 4096 and 16 rows) are loaded before the ring: loads return in issue
-  // order, so X loaded behind the ring would wait for its HBM units, with the ring then idle until the staging ends.
-  constexpr int CPT = UK / 8, XT = 16 / CPT;
-  const uint32_t ng = KS / UK, Mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT, ntask = Mr * ng;
-  u32x4 xr[XT][CPT];
-#pragma unroll
-  for (int i = 0; i < XT; i++) {
-    const uint32_t t = tid + i * GV_NT, m = t / ng, g = t - m * ng;
-#pragma unroll
-    for (int q = 0; q < CPT; q++)
-      xr[i][q] = t < ntask ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q) : (u32x4){0u, 0u, 0u, 0u};
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  MUnit<WE> ring[PF];
-#pragma unroll
-  for (int j = 0; j < PF; j++)
-    if ((uint32_t)j < nuw) load(ring[j], u0 + j);
-  __builtin_amdgcn_sched_barrier(0);
-
-  const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
-  auto stage = [&](uint32_t t, const u32x4 *xin) __attribute__((always_inline)) {
-    const uint32_t m = t / ng, g = t - m * ng;
-    float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int q = 0; q < CPT; q++) {
-      u32x4 xv = xperm<WE>(xin[q]);
-      if constexpr (WE != W_F16) {
-        const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
-        lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
-        hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
-        if constexpr (WE == W_Q4) {
-          xv.y = as_u(b * r16);
-          xv.w = as_u(d * r16);
-        }
-      }
-      *(u32x4 *)(sX + m * KSM + g * UK + 8 * q) = xv;
-    }
-    if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
-    else if constexpr (WE == W_Q8) sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
-  };
-#pragma unroll
-  for (int i = 0; i < XT; i++) {
-    const uint32_t t = tid + i * GV_NT;
-    if (t < ntask) stage(t, xr[i]);
-  }
-  for (uint32_t t = tid + XT * GV_NT; t < ntask; t += GV_NT) {
-    u32x4 xin[CPT];
-    const uint32_t m = t / ng, g = t - m * ng;
-#pragma unroll
-    for (int q = 0; q < CPT; q++) xin[q] = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q);
-    stage(t, xin);
-  }
-  __syncthreads();
-
-  uint32_t j0 = 0;
-#pragma unroll 1
-  for (; j0 + PF <= nuw; j0 += PF) {
+  if constexpr (XS) {
+    // (every ring entry is loaded, clamped to the wave's last unit, so the loads younger than each unit's copy are
+    // counted exactly: LPU weight loads per unit, 2 copies)
+    constexpr int LPU = 8;                                     // q8: 4 code + 4 scale loads; f16: 8 code loads
+    const uint32_t nl = nuw ? nuw - 1u : 0u;
+    MUnit<WE> ring[PF];
 #pragma unroll
     for (int j = 0; j < PF; j++) {
-      compute(ring[j], u0 + j0 + j);
-      const uint32_t nx = j0 + PF + j;
-      load(ring[j], u0 + (nx < nuw ? nx : nuw - 1u));
+      load(ring[j], u0 + ((uint32_t)j < nl ? (uint32_t)j : nl), j);
+      __builtin_amdgcn_sched_barrier(0);
     }
-  }
+    uint32_t j0 = 0;
+#pragma unroll 1
+    for (; j0 + PF <= nuw; j0 += PF) {
 #pragma unroll
-  for (int j = 0; j < PF; j++)
-    if (j0 + j < nuw) compute(ring[j], u0 + j0 + j);
-  __syncthreads();                                             // X' is dead: the buffer takes the partials
+      for (int j = 0; j < PF; j++) {
+        compute_xs(ring[j], j, std::integral_constant<int, LPU + (PF - 1) * (LPU + 2)>{});
+        const uint32_t nx = j0 + PF + j;
+        load(ring[j], u0 + (nx < nuw ? nx : nl), j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    static_assert(PF <= 4, "the tail below covers up to 4 units in flight");
+    auto tail = [&](auto J) __attribute__((always_inline)) {
+      constexpr int j = decltype(J)::value;
+      if constexpr (j < PF)
+        if (j0 + j < nuw) compute_xs(ring[j], j, std::integral_constant<int, LPU + (PF - 1 - j) * (LPU + 2)>{});
+    };
+    tail(std::integral_constant<int, 0>{});
+    tail(std::integral_constant<int, 1>{});
+    tail(std::integral_constant<int, 2>{});
+    tail(std::integral_constant<int, 3>{});
+    __builtin_amdgcn_s_waitcnt(0x0f70);                          // vmcnt(0): no copy may land after this
+    __syncthreads();                                             // the slots are dead: the buffer takes the partials
+  } else {
+  // X' of the slice for the rows < M only (the MFMA A reads of rows past M take zeros instead); one thread per
+    // (row, unit) task stages the unit's chunks and (q4 / q8) its sums of the unscaled X' over the low / high positions
+    // -> (G1, G2); q4: the high-nibble positions (odd pair slots) are stored as x / 16. The chunks of the first XT
+    // tasks of every thread (all of them for K <= 4096 and 16 rows) are loaded before the ring: loads return in issue
+    // order, so X loaded behind the ring would wait for its HBM units, with the ring then idle until the staging ends.
+    constexpr int CPT = UK / 8, XT = 16 / CPT;
+    const uint32_t ng = KS / UK, Mr = p.M < (uint32_t)MT ? p.M : (uint32_t)MT, ntask = Mr * ng;
+    u32x4 xr[XT][CPT];
+  #pragma unroll
+    for (int i = 0; i < XT; i++) {
+      const uint32_t t = tid + i * GV_NT, m = t / ng, g = t - m * ng;
+  #pragma unroll
+      for (int q = 0; q < CPT; q++)
+        xr[i][q] = t < ntask ? xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q) : (u32x4){0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  
+    MUnit<WE> ring[PF];
+  #pragma unroll
+    for (int j = 0; j < PF; j++)
+      if ((uint32_t)j < nuw) load(ring[j], u0 + j);
+    __builtin_amdgcn_sched_barrier(0);
+  
+    const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+    auto stage = [&](uint32_t t, const u32x4 *xin) __attribute__((always_inline)) {
+      const uint32_t m = t / ng, g = t - m * ng;
+      float lo = 0.0f, hi = 0.0f;
+  #pragma unroll
+      for (int q = 0; q < CPT; q++) {
+        u32x4 xv = xperm<WE>(xin[q]);
+        if constexpr (WE != W_F16) {
+          const f16x2 a = as_h2(xv.x), b = as_h2(xv.y), c = as_h2(xv.z), d = as_h2(xv.w);
+          lo += ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
+          hi += ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
+          if constexpr (WE == W_Q4) {
+            xv.y = as_u(b * r16);
+            xv.w = as_u(d * r16);
+          }
+        }
+        *(u32x4 *)(sX + m * KSM + g * UK + 8 * q) = xv;
+      }
+      if constexpr (WE == W_Q4) sG[g * MT + m] = (f32x2){1024.0f * lo + 64.0f * hi, lo + hi};
+      else if constexpr (WE == W_Q8) sG[g * MT + m] = (f32x2){1152.0f * (lo + hi), 0.0f};
+    };
+  #pragma unroll
+    for (int i = 0; i < XT; i++) {
+      const uint32_t t = tid + i * GV_NT;
+      if (t < ntask) stage(t, xr[i]);
+    }
+    for (uint32_t t = tid + XT * GV_NT; t < ntask; t += GV_NT) {
+      u32x4 xin[CPT];
+      const uint32_t m = t / ng, g = t - m * ng;
+  #pragma unroll
+      for (int q = 0; q < CPT; q++) xin[q] = xload8<XM>(p, m, RowCtx{0, 0, 0}, kb0 + g * UK + 8 * q);
+      stage(t, xin);
+    }
+    __syncthreads();
+  
+    uint32_t j0 = 0;
+  #pragma unroll 1
+    for (; j0 + PF <= nuw; j0 += PF) {
+  #pragma unroll
+      for (int j = 0; j < PF; j++) {
+        compute(ring[j], u0 + j0 + j);
+        const uint32_t nx = j0 + PF + j;
+        load(ring[j], u0 + (nx < nuw ? nx : nuw - 1u));
+      }
+    }
+  #pragma unroll
+    for (int j = 0; j < PF; j++)
+      if (j0 + j < nuw) compute(ring[j], u0 + j0 + j);
+    __syncthreads();                                             // X' is dead: the buffer takes the partials
+  
+  }
 
   // D[m = 4 kc + r][row 16 i + l16]
 #pragma unroll
@@ -970,10 +1065,14 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
     }
     if (narrow) {
       if (S != 1 || p.epi == E_HEADS || p.epi == E_ONORMGATE) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((k_gemv_mf<WE, XM, true>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+      if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8))
+        hipLaunchKernelGGL((k_gemv_mf<WE, XM, true, WE != W_Q4 && XM == X_F16>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+      else hipLaunchKernelGGL((k_gemv_mf<WE, XM, true>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
       return hipGetLastError();
     }
-    hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+    if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8))
+      hipLaunchKernelGGL((k_gemv_mf<WE, XM, false, WE != W_Q4 && XM == X_F16>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
+    else hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
   }
   switch (stream_mt(p.M, WE, mx)) {
