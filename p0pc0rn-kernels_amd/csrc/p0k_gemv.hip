@@ -387,7 +387,21 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
   auto stage = [&](uint32_t t, u32x4 v) __attribute__((always_inline)) {
     const uint32_t m = t / nb, kq = t - m * nb;
     v = xperm<WE>(v);
-    if constexpr (WE != W_F16) {
+    if constexpr (WE != W_F16 && MX) {
+      // the unit's X' sum of this row (the 4x4x4 form needs lo + hi only): v_dot2_f32_f16 against ones, 4
+      // instructions instead of 8 conversions and 6 adds (M = 2: 14.0 -> 13.7 us; M = 4 14.6-14.8 -> 14.6)
+      const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+      float t = __builtin_amdgcn_fdot2(as_h2(v.x), one2, 0.0f, false);
+      t = __builtin_amdgcn_fdot2(as_h2(v.y), one2, t, false);
+      t = __builtin_amdgcn_fdot2(as_h2(v.z), one2, t, false);
+      t = __builtin_amdgcn_fdot2(as_h2(v.w), one2, t, false);
+#pragma unroll
+      for (int o = 1; o < UK / 8; o *= 2) t += __shfl_xor(t, o);
+      if (kq % (UK / 8) == 0) sGx[(kq / (UK / 8)) * MT + m] = t;
+      const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
+      v.y = as_u(as_h2(v.y) * r16);
+      v.w = as_u(as_h2(v.w) * r16);
+    } else if constexpr (WE != W_F16) {
       const f16x2 a = as_h2(v.x), b = as_h2(v.y), c = as_h2(v.z), d = as_h2(v.w);
       float lo = ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
       float hi = ((float)b.x + (float)b.y) + ((float)d.x + (float)d.y);
