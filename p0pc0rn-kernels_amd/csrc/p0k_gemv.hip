@@ -395,8 +395,10 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
       t = __builtin_amdgcn_fdot2(as_h2(v.y), one2, t, false);
       t = __builtin_amdgcn_fdot2(as_h2(v.z), one2, t, false);
       t = __builtin_amdgcn_fdot2(as_h2(v.w), one2, t, false);
-#pragma unroll
-      for (int o = 1; o < UK / 8; o *= 2) t += __shfl_xor(t, o);
+      static_assert(UK / 8 == 4, "a unit's chunks are one lane quad");
+      // sum over the lane quad by DPP quad permutes (xor 1, then xor 2; M = 4 14.65-14.74 -> 14.32-14.58 us)
+      t += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
+      t += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
       if (kq % (UK / 8) == 0) sGx[(kq / (UK / 8)) * MT + m] = t;
       const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
       v.y = as_u(as_h2(v.y) * r16);
