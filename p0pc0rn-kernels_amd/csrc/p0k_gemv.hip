@@ -403,6 +403,16 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
       const f16x2 r16 = {(f16)0.0625f, (f16)0.0625f};
       v.y = as_u(as_h2(v.y) * r16);
       v.w = as_u(as_h2(v.w) * r16);
+    } else if constexpr (WE == W_Q4) {
+      // (lo, hi) by v_dot2 against ones and DPP quad sums, as above (q4 N 4096 K 4096 at one row: 6.19 -> 6.11 us)
+      const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+      float lo = __builtin_amdgcn_fdot2(as_h2(v.z), one2, __builtin_amdgcn_fdot2(as_h2(v.x), one2, 0.0f, false), false);
+      float hi = __builtin_amdgcn_fdot2(as_h2(v.w), one2, __builtin_amdgcn_fdot2(as_h2(v.y), one2, 0.0f, false), false);
+      lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0xB1, 0xF, 0xF, false));
+      hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0xB1, 0xF, 0xF, false));
+      lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0x4E, 0xF, 0xF, false));
+      hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0x4E, 0xF, 0xF, false));
+      if (kq % (UK / 8) == 0) sG[m * NGM + kq / (UK / 8)] = (f32x2){lo, hi};
     } else if constexpr (WE != W_F16) {
       const f16x2 a = as_h2(v.x), b = as_h2(v.y), c = as_h2(v.z), d = as_h2(v.w);
       float lo = ((float)a.x + (float)a.y) + ((float)c.x + (float)c.y);
