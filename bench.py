@@ -63,7 +63,7 @@ MALL = 256 << 20
 # headline's are measured by child rocprofv3 runs at the start of the bench (measure_traffic); for the other
 # workloads, and when rocprofv3 is not available, the figures of the last profiled build are kept here.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36010, 28), "decode_q4_swiglu_M4": (36136, 112), "decode_q4_swiglu_M16": (37299, 448),
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
                "decode_q4_plain_M1": (18022, 28), "decode_q4_plain_N4096_M1": (5203, 8),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
