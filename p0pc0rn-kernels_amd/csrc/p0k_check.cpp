@@ -283,7 +283,10 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
       // 21.3 at 8 rows and N 6144; so they stay split)
       const uint32_t kq8 = gemv_unit_k(we, mf) * 8u;   // k of one unit in each K-eighth
       const bool fill = 2 * tiles128 >= tune.cus * 7u / 8u;
-      const bool short_k = we == P0K_ENC_Q4G32A_T64 && (uint64_t)K * 40u <= 256u * 1024u;
+      // (q8 too, items up to 288 KB, with X streamed per unit: q8 N 4096 K 4096 10.7 -> 9.5 us, N 6144 17.0 -> 9.8,
+      // N 4096 K 2048 9.95 -> 6.9; f16 items stream slowly one per CU, 15.3 -> 17.6 us at N 4096 K 2048)
+      const bool short_k = (we == P0K_ENC_Q4G32A_T64 && (uint64_t)K * 40u <= 256u * 1024u) ||
+                           (we == P0K_ENC_Q8G64S_T64 && (uint64_t)K * 66u <= 288u * 1024u);
       if (tune.gemv_narrow && S >= 2 && (mf || (we == P0K_ENC_Q4G32A_T64 && M <= 4)) && epi != P0K_EPI_HEADS &&
           epi != P0K_EPI_ONORMGATE && (fill || short_k) && K <= gemv_ks_max(M, we, mf, mx) && K % kq8 == 0) {
         narrow = true;

@@ -1091,12 +1091,15 @@ static hipError_t launch2(const Params &p, float *part, uint32_t *cnt, uint32_t 
     }
     if (narrow) {
       if (S != 1 || p.epi == E_HEADS || p.epi == E_ONORMGATE) return hipErrorInvalidValue;
-      if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8))
+      if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8) && KS / 64u / (2u * GV_KSUB) >= (uint32_t)MUnit<WE>::PF)
         hipLaunchKernelGGL((k_gemv_mf<WE, XM, true, WE != W_Q4 && XM == X_F16>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
       else hipLaunchKernelGGL((k_gemv_mf<WE, XM, true>), dim3((p.N + 63) / 64), dim3(GV_NT), 0, s, p, part, cnt, S, KS);
       return hipGetLastError();
     }
-    if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8))
+    // (streamed X when every ring entry of a wave holds one of its units: the ring is filled unconditionally, so a
+    // shorter stream would load its last unit again per empty entry; f16 N 4096 K 2048 in 8 slices, one unit per
+    // wave: 15.3 us streamed against 11.5 staged)
+    if (WE != W_Q4 && XM == X_F16 && (p.flags & F_XALIGN8) && KS / 64u / GV_KSUB >= (uint32_t)MUnit<WE>::PF)
       hipLaunchKernelGGL((k_gemv_mf<WE, XM, false, WE != W_Q4 && XM == X_F16>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     else hipLaunchKernelGGL((k_gemv_mf<WE, XM>), grid, dim3(GV_NT), 0, s, p, part, cnt, S, KS);
     return hipGetLastError();
