@@ -65,7 +65,7 @@ MALL = 256 << 20
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
-               "decode_q4_plain_M1": (18022, 28), "decode_q4_plain_N4096_M1": (5203, 8),
+               "decode_q4_plain_M1": (18022, 28), "decode_q4_plain_N4096_M1": (5203, 8), "decode_q8_plain_M1": (30285, 28),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
                "dit_qkv_q4_lnmod_heads": (132057, 98304), "dit_up_q4_geglu": (250822, 98304),
@@ -93,22 +93,22 @@ class Workload:
         self.M, self.args, self.bufs, self.extra, self.kind = M, args, bufs, extra or {}, kind
 
 
-def decode_q4(dev, M, copies=None, glu=True, n_out=14336):
+def decode_q4(dev, M, copies=None, glu=True, n_out=14336, enc="q4g32a.t64"):
     """q4 GEMV decode, out 14336 with SwiGLU (weight rows [gate 14336 | up 14336]), K 4096; glu=False:
     the plain q4 GEMV N n_out with the f16 epilogue (14336: 36.7 MB of weights; 4096: the same model's attention
-    projection, 10.5 MB)."""
+    projection, 10.5 MB); enc: the same plain GEMV with q8 weights (decode of a q8-encoded model)."""
     N_out, K = n_out, 4096
     rows = 2 * N_out if glu else N_out
     r = rng(1)
     W = (r.standard_normal((rows, K), dtype=np.float32) * np.float32(0.02))
-    wb = p0k.pack("q4g32a.t64", W, rows, K)
+    wb = p0k.pack(enc, W, rows, K)
     del W
     copies = copies or max(4, -(-(2 * MALL) // wb.nbytes))
     bufs = [dev.upload(wb) for _ in range(copies)]
     x = dev.upload(f16(r.standard_normal(M * K)))
     y = dev.buffer(M * N_out * 2)
     bufs += [x, y]
-    args = [{"w": {"enc": "q4g32a.t64", "buf": b, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
+    args = [{"w": {"enc": enc, "buf": b, "off": 0, "bytes": wb.nbytes, "rows": rows, "cols": K},
              "x": {"buf": x}, "y": {"buf": y, "ld": N_out}, "M": M, "N": rows, "K": K, "epi": "swiglu", "wr0": 0,
              "wr1": N_out} for b in bufs[:copies]]
     if not glu:
@@ -117,8 +117,9 @@ def decode_q4(dev, M, copies=None, glu=True, n_out=14336):
             del a["wr1"]
     nbytes = wb.nbytes + M * K * 2 + M * N_out * 2
     if not glu:
-        name = f"decode_q4_plain_M{M}" if N_out == 14336 else f"decode_q4_plain_N{N_out}_M{M}"
-        return Workload(name, f"q4 GEMV, M={M}, N={N_out}, K={K}, f16 epilogue", "hbm",
+        wn = "q4" if enc == "q4g32a.t64" else "q8"
+        name = f"decode_{wn}_plain_M{M}" if N_out == 14336 else f"decode_{wn}_plain_N{N_out}_M{M}"
+        return Workload(name, f"{wn} GEMV, M={M}, N={N_out}, K={K}, f16 epilogue", "hbm",
                         2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
     return Workload(f"decode_q4_swiglu_M{M}", f"q4 GEMV + SwiGLU, M={M}, out {N_out}, weight rows {rows}, K={K}",
                     "hbm", 2.0 * M * rows * K, nbytes, M, args, bufs, {"weight_copies": copies, "weight_bytes": wb.nbytes})
@@ -286,6 +287,7 @@ BUILDERS = {
     "decode2": lambda d: decode_q4(d, 2), "decode8": lambda d: decode_q4(d, 8),
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "decode1_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096),
+    "decode1_q8": lambda d: decode_q4(d, 1, glu=False, enc="q8g64s.t64"),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
     "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
 }
@@ -704,8 +706,10 @@ def main():
         "value": head["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": head["calls"], "warmup": a.warmup,
         "ms_per_step": head["ms_per_call"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4 weights (u4 codes -> fp16), fp16 activations, fp32 accumulate", "data": "synthetic (seeded PCG64)",
-        "config": {"workload": head["name"], "M": head["M"], "N": 28672, "K": 4096, "enc": "q4g32a.t64", "epi": "swiglu",
-                   "weight_copies_rotated": head.get("weight_copies")},
+        "config": ({"workload": head["name"], "M": head["M"], "N": 28672, "K": 4096, "enc": "q4g32a.t64", "epi": "swiglu",
+                    "weight_copies_rotated": head.get("weight_copies")} if head is results.get("decode1") else
+                   {"workload": head["name"], "M": head["M"], "desc": head["desc"],
+                    "weight_copies_rotated": head.get("weight_copies")}),
         "roofline": (dict(head["roofline"], traffic=live_traffic["bytes"], traffic_source="rocprofv3 FETCH_SIZE + "
                           "WRITE_SIZE of the headline kernel in this run, scaled by a 1 GiB copy's counts")
                      if live_traffic and head is results.get("decode1") else
