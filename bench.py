@@ -65,7 +65,7 @@ MALL = 256 << 20
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
-               "decode_q4_plain_M1": (18022, 28), "decode_q4_plain_N4096_M1": (5203, 8), "decode_q8_plain_M1": (30285, 28),
+               "decode_q4_plain_M1": (18014, 28), "decode_q4_plain_N4096_M1": (5199, 8), "decode_q8_plain_M1": (30285, 28),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
                "dit_qkv_q4_lnmod_heads": (132057, 98304), "dit_up_q4_geglu": (250822, 98304),
