@@ -9,9 +9,10 @@ every other config under "workloads", each with its own roofline fraction: decod
 N 14336, q8 prefill with RMSNorm + fp32 residual add (and its fp16-residual `bias` + `res` variant, and the rowstats
 pass it needs, timed on its own), the DiT QKV / GeGLU GEMMs, conv3 and the attention consumer.
 
-Timing: the timed calls are captured once in a HIP graph on the library's stream and replayed; HIP events on that
-stream bracket the replays (p0k_sync before and after), one before each replay, so every workload also reports the
-p10 / median / p90 of its per-call time over the replays. For the HBM-bound decode the calls rotate through enough
+Timing: the timed calls are plain launches on the library's stream, enqueued behind a gate kernel (a bounded wait on
+the GPU) so that the warmup calls run straight into the timed ones and the calls run back to back; HIP events on that
+stream bracket them, one after every group of calls, so every workload also reports the p10 / median / p90 of its
+per-call time over the groups. For the HBM-bound decode the calls rotate through enough
 weight copies (> 256 MB) that no call finds its weights in the MALL. Inputs come from numpy's PCG64 generator with
 fixed seeds, encoded with libp0k's own FORMAT.md encoders (BASELINE.json value recipes).
 
@@ -22,18 +23,18 @@ weight decode plus a few rows of M, scaled linearly in M (the cost is exactly li
 
     python bench.py --mfma-ceiling
 
-the matrix-core ceilings: how many VALU instructions per 32x32x16 MFMA a loop can hide (p0k_mfma_valu_probe) with
+the matrix-core ceilings: how many VALU instructions per 32x32x16 MFMA a loop can hide (p0kprobe_mfma_valu) with
 constant operands, the rate the matrix cores sustain on random operands (the clock under a full MFMA load), and the
 vendor library's plain fp16 GEMM at the configs' shapes for scale.
 
     python bench.py --hbm-ceiling
 
-the streaming-read ceiling of the headline's 73.4 MB over several launch shapes (p0k_stream_read_probe).
+the streaming-read ceiling of the headline's 73.4 MB over several launch shapes (p0kprobe_stream_read).
 
     python bench.py --lds-ceiling
 
 the LDS read bandwidth of one CU (bytes per shader clock) and the clock the part held, with 4, 8 and 16 waves
-(p0k_lds_read_probe).
+(p0kprobe_lds_read).
 
     python bench.py --copy-calib
 
@@ -51,7 +52,9 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "p0pc0rn-kernels_amd", "python"))
+sys.path.insert(0, os.path.join(ROOT, "p0pc0rn-kernels_amd", "probe"))
 import p0k  # noqa: E402
+import probe  # noqa: E402      the measurement kernels (libp0k_probe.so): ceilings and the launch gate
 
 HBM_PEAK = 8.0e12          # B/s, MI355X published
 FP16_PEAK = 2.5e15         # FLOP/s dense fp16 MFMA, MI355X published
@@ -63,7 +66,7 @@ MALL = 256 << 20
 # headline's are measured by child rocprofv3 runs at the start of the bench (measure_traffic); for the other
 # workloads, and when rocprofv3 is not available, the figures of the last profiled build are kept here.
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
-TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
+TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M1_long": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
                "decode_q4_plain_M1": (18014, 28), "decode_q4_plain_N4096_M1": (5199, 8), "decode_q8_plain_M1": (30285, 28),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
@@ -268,7 +271,7 @@ def dit_attn(dev):
 
 
 def hbm_ceiling(dev, blocks=0, threads=512):
-    """the measured HBM read ceiling for the headline: a plain streaming read (p0k_stream_read_probe, nothing computed or
+    """the measured HBM read ceiling for the headline: a plain streaming read (p0kprobe_stream_read, nothing computed or
     stored) of as many bytes as the q4 decode's weights (73,400,320), rotated over the same number of copies; by default
     with the decode GEMV's grid (blocks 0: 7/8 of the CUs, 512 threads)"""
     nbytes = 28672 // 64 * (4096 // 32) * 1280
@@ -282,8 +285,15 @@ def hbm_ceiling(dev, blocks=0, threads=512):
                     nbytes, 1, args, bufs + [sink], {"weight_copies": copies}, kind="probe")
 
 
+def renamed(wl, name, desc):
+    wl.name, wl.desc = name, desc
+    return wl
+
+
 BUILDERS = {
-    "decode1": lambda d: decode_q4(d, 1), "hbm_ceiling": hbm_ceiling, "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
+    "decode1": lambda d: decode_q4(d, 1), "hbm_ceiling": hbm_ceiling,
+    "decode1_long": lambda d: renamed(decode_q4(d, 1), "decode_q4_swiglu_M1_long",
+                                      "the headline workload over a long run (at least 2000 calls, events every 64)"), "decode4": lambda d: decode_q4(d, 4), "decode16": lambda d: decode_q4(d, 16),
     "decode2": lambda d: decode_q4(d, 2), "decode8": lambda d: decode_q4(d, 8),
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "decode1_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096),
@@ -294,9 +304,21 @@ BUILDERS = {
 
 
 # ------------------------------------------------------------------------------------------------ timing
-def time_workload(dev, wl, steps, warmup):
-    L = p0k.lib()
+GATE_MIN_US = 200          # the launch gate ahead of each timed region: at least this long, and longer than the host
+GATE_MAX_US = 100000       # takes to enqueue the region's calls (measured per call before the region)
+
+
+def time_workload(dev, wl, steps, warmup, single=False):
+    """Time exactly `steps` calls of the workload (rotating over its argument sets), `warmup` untimed calls right
+    before them. The calls are plain launches on the library's stream (a serving loop's calls): a gate kernel first
+    holds the GPU while this thread enqueues the warmup calls, an event, the timed calls and an event, so on the GPU
+    the warmup calls run straight into the timed ones and every call starts as its predecessor ends, with no host
+    launch latency inside the timed region. (Replaying the same calls from a HIP graph measured 0.1-0.4 us per call
+    slower on this part.) Events after every `group` timed calls (64 for memory-bound lines, 8 otherwise) give the
+    per-call distribution; single: one group of all `steps` calls (the headline and its ceiling).
+    Returns (ms per call from the events, wall ms per call, calls, distribution, gate facts)."""
     import ctypes as C
+    L = p0k.lib()
     if wl.kind == "attn":
         structs = [p0k.attn_args(a, dev.resolve) for a in wl.args]
         run = dev.attention_raw
@@ -304,7 +326,7 @@ def time_workload(dev, wl, steps, warmup):
             p0k._chk(L.p0k_attention_check(C.byref(s)))
     elif wl.kind == "probe":
         structs = wl.args
-        run = lambda a: dev.stream_read_probe(a["buf"], a["bytes"], a["sink"], a["blocks"], a["threads"])   # noqa: E731
+        run = lambda a: probe.stream_read(dev, a["buf"], a["bytes"], a["sink"], a["blocks"], a["threads"])   # noqa: E731
     elif wl.kind == "rowstats":
         structs = wl.args
         run = lambda a: dev.rowstats(a["x"], a["rows"], a["cols"], a["mode"], a["eps"], a["st"])   # noqa: E731
@@ -313,72 +335,54 @@ def time_workload(dev, wl, steps, warmup):
         run = dev.gemm_raw
         for s in structs:
             p0k._chk(L.p0k_gemm_check(C.byref(s)))
+    n_arg = len(structs)
     for s in structs:
-        run(s)                          # one eager call per shape first: sizes the workspace before capture
+        run(s)                          # one call per argument set first: sizes the workspaces
     dev.done()
-    if os.environ.get("P0K_BENCH_EAGER"):            # profiling: plain launches, no graph
-        e0, e1 = dev.event(), dev.event()
-        dev.record(e0)
-        for i in range(steps):
-            run(structs[i % len(structs)])
-        dev.record(e1)
-        dev.done()
-        ms = dev.elapsed_ms(e0, e1) / steps
-        dev.event_destroy(e0)
-        dev.event_destroy(e1)
-        return ms, ms, steps, None
-    # exactly `steps` timed calls: `reps` replays of a graph of `per_graph` calls (a multiple of the rotation), then
-    # one replay of a graph with the remaining calls; the per-call distribution comes from the full replays
-    per_graph = max(len(structs), min(steps, 64 if wl.bound == "hbm" else 8))
-    per_graph -= per_graph % len(structs)
-    reps, rem = divmod(steps, per_graph)
-    if reps == 0:
-        reps, rem, per_graph = 1, 0, steps
-
-    def capture(n, first):
-        dev.graph_begin()
-        try:
-            for i in range(n):
-                run(structs[(first + i) % len(structs)])
-        finally:
-            g = dev.graph_end()
-        return g
-    g = capture(per_graph, 0)
-    gr = capture(rem, reps * per_graph) if rem else None
-    wreps, wrem = divmod(warmup, per_graph)                 # exactly `warmup` untimed calls
-    for _ in range(wreps):
-        dev.graph_launch(g)
-    if wrem:
-        gw = capture(wrem, 0)
-        dev.graph_launch(gw)
-        dev.done()
-        dev.graph_destroy(gw)
+    probe_calls = max(8, 2 * n_arg)     # the host's enqueue cost per call, for the gate's length
+    t = time.perf_counter()
+    for i in range(probe_calls):
+        run(structs[i % n_arg])
+    enq_s = (time.perf_counter() - t) / probe_calls
     dev.done()
-    # one event before each replay and one after the last: the whole timed region, and per replay the time per call
-    ev = [dev.event() for _ in range(reps + 2)]
+    group = steps if single else max(1, min(steps, 64 if wl.bound == "hbm" else 8))
+    groups, rem = divmod(steps, group)
+    gate_us = int(min(GATE_MAX_US, max(GATE_MIN_US, 2.0 * (warmup + steps) * enq_s * 1e6 + 100)))
+    ev = [dev.event() for _ in range(groups + 2)]
+    sink = dev.buffer(16)
+    probe.gate(dev, 1, sink)            # the gate's code object is loaded at its first launch: not inside the region
+    dev.done()
     t0 = time.perf_counter()
+    probe.gate(dev, gate_us, sink)
+    for i in range(warmup):
+        run(structs[i % n_arg])
     dev.record(ev[0])
-    for i in range(reps):
-        dev.graph_launch(g)
-        dev.record(ev[i + 1])
-    if gr is not None:
-        dev.graph_launch(gr)
+    k = warmup
+    for gi in range(groups):
+        for _ in range(group):
+            run(structs[k % n_arg])
+            k += 1
+        dev.record(ev[gi + 1])
+    for _ in range(rem):
+        run(structs[k % n_arg])
+        k += 1
     dev.record(ev[-1])
+    t_enq = time.perf_counter() - t0
     dev.done()
     wall = time.perf_counter() - t0
+    dev.free(sink)
     ms = dev.elapsed_ms(ev[0], ev[-1])
-    per = sorted(dev.elapsed_ms(ev[i], ev[i + 1]) / per_graph for i in range(reps))
+    per = sorted(dev.elapsed_ms(ev[i], ev[i + 1]) / group for i in range(groups))
     for e in ev:
         dev.event_destroy(e)
-    dev.graph_destroy(g)
-    if gr is not None:
-        dev.graph_destroy(gr)
-    n = reps * per_graph + rem
-    assert n == steps
-    q = lambda f: per[min(reps - 1, int(f * reps))]   # noqa: E731
-    dist = {"p10": round(q(0.1), 5), "median": round(q(0.5), 5), "p90": round(q(0.9), 5), "replays": reps,
-            "calls_per_replay": per_graph, "remainder_calls": rem}
-    return ms / n, wall / n * 1e3, n, dist
+    assert k - warmup == steps
+    gate = {"gate_us": gate_us, "host_enqueue_us": round(t_enq * 1e6, 1), "gate_covered_enqueue": t_enq * 1e6 < gate_us}
+    if not gate["gate_covered_enqueue"]:
+        log(f"{wl.name}: the host took {t_enq * 1e6:.0f} us to enqueue, longer than the {gate_us} us gate")
+    q = lambda f: per[min(groups - 1, int(f * groups))]   # noqa: E731
+    dist = None if single else {"p10": round(q(0.1), 5), "median": round(q(0.5), 5), "p90": round(q(0.9), 5),
+                                "groups": groups, "calls_per_group": group, "remainder_calls": rem}
+    return ms / steps, wall / steps * 1e3, steps, dist, gate
 
 
 def roofline(wl, ms):
@@ -409,7 +413,7 @@ def _pmc_mean(counter, args, kernel, timeout=150):
     if not exe:
         return None
     d = tempfile.mkdtemp(prefix="p0k_pmc_", dir="/tmp")
-    env = dict(os.environ, TMPDIR="/tmp", P0K_BENCH_EAGER="1")
+    env = dict(os.environ, TMPDIR="/tmp")
     try:
         r = subprocess.run([exe, "--pmc", counter, "-d", d, "-o", "run", "--output-format", "csv", "--",
                             sys.executable, os.path.abspath(__file__)] + args, cwd="/tmp", env=env,
@@ -468,6 +472,8 @@ def cpu_baseline(config, rows, target_s=0.0):
 
 
 HBM_SECONDARY_CALLS = 1000   # timed calls of each memory-bound workload other than the headline (at least)
+LONG_RUN_CALLS = 2000        # timed calls of the headline's long-run line (at least)
+SINGLE = ("decode1", "hbm_ceiling")   # timed as one group of exactly --steps calls (the headline and its ceiling)
 CPU_HEADLINE_S = 10.0   # seconds of CPU work timed for the headline workload (whole calls, repeated)
 CPU_SAMPLE = {   # workload -> (cpu_ref config, rows of M timed)
     "decode_q4_swiglu_M1": ("decode", 1), "decode_q4_swiglu_M4": ("decode", 4), "decode_q4_swiglu_M16": ("decode", 8),
@@ -488,12 +494,12 @@ def copy_calib(nbytes=1 << 30, reps=5):
 
 
 def mfma_probe_rate(dev, sink, v, wps, iters, rnd):
-    """one timed launch of p0k_mfma_valu_probe (after a short untimed one): (ms, TFLOP/s, fraction of the peak)"""
-    dev.mfma_valu_probe(v, wps, 10, sink, rnd)
+    """one timed launch of p0kprobe_mfma_valu (after a short untimed one): (ms, TFLOP/s, fraction of the peak)"""
+    probe.mfma_valu(dev, v, wps, 10, sink, rnd)
     dev.done()
     e0, e1 = dev.event(), dev.event()
     dev.record(e0)
-    dev.mfma_valu_probe(v, wps, iters, sink, rnd)
+    probe.mfma_valu(dev, v, wps, iters, sink, rnd)
     dev.record(e1)
     dev.done()
     ms = dev.elapsed_ms(e0, e1)
@@ -505,7 +511,7 @@ def mfma_probe_rate(dev, sink, v, wps, iters, rnd):
 
 def lds_ceiling(dev, iters=4096):
     """`--lds-ceiling`: LDS read bandwidth of one CU with 4, 8 and 16 waves issuing conflict-free 16-byte reads
-    (p0k_lds_read_probe, one workgroup per CU, all CUs). Each wave records the shader clock and the 100 MHz reference
+    (p0kprobe_lds_read, one workgroup per CU, all CUs). Each wave records the shader clock and the 100 MHz reference
     clock around its loop; per CU the loop runs from its first wave's start to its last wave's end, so the line gives
     bytes per shader clock of a CU and the clock the part held, averaged over the CUs of the second launch."""
     cus = dev.cus()
@@ -513,7 +519,7 @@ def lds_ceiling(dev, iters=4096):
     rows = []
     for waves in (4, 8, 16):
         for _ in range(2):                                   # the first launch warms up, the second is read
-            dev.lds_read_probe(waves, iters, clk)
+            probe.lds_read(dev, waves, iters, clk)
             dev.done()
         t = dev.read(clk, np.uint64, 4 * waves * cus).reshape(cus, waves, 4).astype(np.float64)
         cyc = t[:, :, 1].max(axis=1) - t[:, :, 0].min(axis=1)
@@ -525,12 +531,12 @@ def lds_ceiling(dev, iters=4096):
         log(f"lds ceiling, {waves} waves: {rows[-1]}")
     dev.free(clk)
     print(json.dumps({"lds_read_ceiling": rows, "what": "16-byte conflict-free LDS reads per lane, one workgroup per "
-                      "CU, all CUs (p0k_lds_read_probe)", "iters": iters}), flush=True)
+                      "CU, all CUs (p0kprobe_lds_read)", "iters": iters}), flush=True)
 
 
 def mfma_ceiling(dev):
     """`--mfma-ceiling`: FLOP rate of 8 independent 32x32x16 fp16 MFMAs per iteration with V packed-fp16 FMAs per
-    MFMA, one and two waves per SIMD (p0k_mfma_valu_probe), timed with events on the library's stream; first with
+    MFMA, one and two waves per SIMD (p0kprobe_mfma_valu), timed with events on the library's stream; first with
     sparse constant operands (the issue rate), then with pseudo-random operands over about 50 ms per launch (the rate
     the part sustains on real data: the matrix cores' power draw sets the clock). Last, for scale, the vendor library's
     plain fp16 GEMM (torch.matmul -> hipBLASLt, no dequant, no prologue / epilogue) at the configs' shapes."""
@@ -590,7 +596,7 @@ def hbm_ceiling_sweep(dev, steps, warmup):
     rows = []
     for blocks, threads in ((0, 512), (256, 512), (512, 512), (512, 256), (1024, 256), (2048, 256)):
         wl = hbm_ceiling(dev, blocks, threads)
-        ms, _, _, dist = time_workload(dev, wl, steps, warmup)
+        ms, _, _, dist, _ = time_workload(dev, wl, steps, warmup)
         rows.append({"blocks": blocks or dev.cus() * 7 // 8, "threads": threads, "ms_per_call": round(ms, 5),
                      "gbps": round(wl.algo_bytes / ms / 1e6, 1), "frac": round(wl.algo_bytes / (ms * 1e-3) / HBM_PEAK, 4),
                      "median_ms": dist["median"] if dist else None})
@@ -649,11 +655,19 @@ def main():
     for n in names:
         wl = BUILDERS[n](dev)
         # the headline runs exactly --steps calls; the other memory-bound lines (10-20 us per call) at least
-        # HBM_SECONDARY_CALLS, so that one slow graph replay of a short burst does not decide their mean
-        steps = (a.steps if n == "decode1" else max(a.steps, HBM_SECONDARY_CALLS)) if wl.bound == "hbm" else max(10, a.steps // 10)
-        ms, wall_ms, count, dist = time_workload(dev, wl, steps, a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10))
+        # HBM_SECONDARY_CALLS, so that one slow group of a short burst does not decide their mean
+        if wl.bound != "hbm":
+            steps = max(10, a.steps // 10)
+        elif n in SINGLE:
+            steps = a.steps
+        else:
+            steps = max(a.steps, LONG_RUN_CALLS if n == "decode1_long" else HBM_SECONDARY_CALLS)
+        ms, wall_ms, count, dist, gate = time_workload(dev, wl, steps,
+                                                       a.warmup if wl.bound == "hbm" else max(2, a.warmup // 10),
+                                                       single=n in SINGLE)
         rf = roofline(wl, ms)
         res = {"name": wl.name, "desc": wl.desc, "M": wl.M, "ms_per_call": round(ms, 5), "calls": count,
+               "wall_ms_per_call": round(wall_ms, 5), "gate": gate,
                "ms_per_call_dist": dist,
                "tflops": round(wl.flops / ms / 1e9, 3), "gbps": round(wl.algo_bytes / ms / 1e6, 1),
                "algo_bytes": wl.algo_bytes, "flops": wl.flops, "roofline": rf, **wl.extra}
@@ -670,7 +684,7 @@ def main():
         ms, tf, fr = mfma_probe_rate(dev, sink, 0, 2, 20000, True)
         dev.free(sink)
         mceil = {"what": "8 independent 32x32x16 fp16 MFMAs per iteration on pseudo-random operands, two waves per "
-                         "SIMD, all CUs, one launch (p0k_mfma_valu_probe)", "ms": round(ms, 3), "tflops": tf, "frac": fr}
+                         "SIMD, all CUs, one launch (p0kprobe_mfma_valu)", "ms": round(ms, 3), "tflops": tf, "frac": fr}
         log(f"mfma ceiling (random operands): {tf} TFLOP/s ({fr})")
         for r in results.values():
             if r["roofline"]["bound"] == "mfma":
@@ -699,7 +713,6 @@ def main():
                 res["x_vs_cpu"] = round(cpu_ms / res["ms_per_call"], 1)
                 log(f"cpu {res['name']}: {cpu_ms:.1f} ms/call ({sample}) -> x{res['x_vs_cpu']}")
     head = results.get("decode1") or next(iter(results.values()))
-    hw = {k: v for k, v in head.items() if k not in ("roofline", "cpu")}
     cpu = head.get("cpu")
     line = {
         "metric": "q4/q8 GEMM TFLOP/s + HBM GB/s (% roofline) at M=1 and M=4096; x vs CPU ref",
@@ -720,14 +733,18 @@ def main():
                           "sample": f"{cpu['sample']}; oracle/cpu_ref.mjs on Node {cpu['node']}, one thread of "
                                     f"{cpu['host_cores']} host cores ({cpu['cpu_model']})"} if cpu else None),
         "measured_ceiling": ({"what": "plain streaming read of the headline's weight bytes, same launch shape and "
-                                      "graph timing (p0k_stream_read_probe)", "ms_per_call": results["hbm_ceiling"]["ms_per_call"],
+                                      "timing (p0kprobe_stream_read)", "ms_per_call": results["hbm_ceiling"]["ms_per_call"],
                               "gbps": results["hbm_ceiling"]["gbps"],
                               "headline_vs_ceiling": round(results["hbm_ceiling"]["ms_per_call"] / head["ms_per_call"], 4)}
                              if "hbm_ceiling" in results and head is results.get("decode1") else None),
         "measured_mfma_ceiling": mceil,
         "device": info["name"],
         "workloads": list(results.values()),
-        "wall_ms_per_step": round(hw.get("ms_per_call", 0), 5),
+        "wall_ms_per_step": round(head["wall_ms_per_call"], 5),
+        "timing": {"events": "HIP events on the library's stream around the timed calls (plain launches, enqueued "
+                             "behind a gate kernel so they run back to back)", "gate": head["gate"],
+                   "wall": "host clock from the gate's launch to the end of the synchronisation after the last call, "
+                           "per call (includes the gate and the warmup calls)"},
     }
     print(json.dumps(line), flush=True)
 

@@ -39,8 +39,9 @@
 extern "C" {
 #endif
 
-/* 2: p0k_stream_read_probe takes the workgroup size, p0k_mfma_valu_probe the operand pattern; 3: p0k_lds_read_probe */
-#define P0K_ABI_VERSION 3
+/* 4: the measurement probes moved to the benchmark's own library; p0k_ctx_stream, p0k_gemm_plan,
+ *    p0k_ctx_workspace_stats added */
+#define P0K_ABI_VERSION 4
 
 /* ---- status codes */
 enum {
@@ -179,6 +180,12 @@ int p0k_device_info_get(p0k_ctx *ctx, p0k_device_info *out);
  * src/core/tune.js:30-36). p0k_ctx_cus: the CU count the context plans for. */
 int p0k_ctx_reload_env(p0k_ctx *ctx);
 int p0k_ctx_cus(p0k_ctx *ctx);
+/* The context's HIP stream (a hipStream_t), for callers that enqueue their own work in order with the context's (no
+ * counterpart in the reference, whose queue is gpu.device.queue, src/core/gpu.js:15-20). */
+void *p0k_ctx_stream(p0k_ctx *ctx);
+/* Device bytes held by the context's gemm workspaces (split-decode partials, the rms / lnmod X'), and how many
+ * replaced workspaces it keeps because a graph captured after they were allocated may still address them. */
+int p0k_ctx_workspace_stats(p0k_ctx *ctx, uint64_t *live_bytes, uint64_t *retired_buffers);
 
 /* ---- buffers */
 /* alloc / free return P0K_E_ARG while the context's stream is being captured into a graph (a clear or a hipFree
@@ -201,12 +208,16 @@ double p0k_gemm_flops(const p0k_gemm_args *a);                 /* 2*M*N*K, the r
  * same kernels, with every workspace (split-decode partials and counters, the rms / lnmod / PixelNorm X', the conv3
  * zero block) taken from one static device array per GPU, set up when the first context on that GPU is created.
  * A call needing more than p0k_gemm_noalloc_scratch_bytes() (31.5 MiB: e.g. X' of M * K * 2 bytes) is refused with
- * P0K_E_ARG. All calls on one GPU share the array, so calls that overlap in time on one GPU (other streams, other
- * contexts) race; calls in order on one stream do not. Results are the same bits as p0k_gemm's. */
+ * P0K_E_ARG. The first context that calls it on a GPU holds that GPU's array until the context is destroyed, and calls
+ * from any other context on the GPU are refused with P0K_E_ARG (their stream could overlap the holder's calls). Calls
+ * in order on the holder's stream do not race; each call may overwrite what the previous one left in the array.
+ * Results are the same bits as p0k_gemm's. */
 int p0k_gemm_noalloc(p0k_ctx *ctx, const p0k_gemm_args *a);
 uint64_t p0k_gemm_noalloc_scratch_bytes(void);
-int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm will use (for a
-                                                                   256-CU device and the current environment) */
+int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out);     /* the kernel and tile p0k_gemm would use on a
+                                                                   256-CU device with the current environment */
+int p0k_gemm_plan(p0k_ctx *ctx, const p0k_gemm_args *a, p0k_tile *out);   /* the kernel and tile p0k_gemm uses on
+                                                                   this context (its CU count and tuning switches) */
 int p0k_rowstats_check(const p0k_rowstats_args *a);
 int p0k_rowstats(p0k_ctx *ctx, const p0k_rowstats_args *a);
 
@@ -225,26 +236,6 @@ int p0k_gn_partial(p0k_ctx *ctx, const p0k_gn_args *a, uint32_t *nwg_out);
 int p0k_gn_finalize(p0k_ctx *ctx, const p0k_gn_args *a);
 /* groupnormStats(gpu, a)         src/ops/misc.js:106   partial rows of the whole tensor, then finalize */
 int p0k_groupnorm_stats(p0k_ctx *ctx, const p0k_gn_args *a);
-
-/* ---- measurement: the HBM read ceiling (no counterpart in the reference). Reads `bytes` of a live buffer with
- *      `blocks` workgroups of `threads` (256 or 512) threads (blocks 0 = 7/8 of the CUs, the decode GEMV's grid for
- *      28672 weight rows), 16-byte loads, eight in flight per lane, nothing stored (sink: a live 4-byte buffer the
- *      kernel may write; bytes below 4 GiB); the time per call is what the decode GEMV's algorithmic bytes are
- *      compared with. */
-int p0k_stream_read_probe(p0k_ctx *ctx, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks, uint32_t threads);
-/*      the matrix-core issue ceiling (no counterpart in the reference): one 256-thread workgroup per CU per wave per
- *      SIMD (waves_per_simd 1 or 2), `iters` iterations of 8 independent 32x32x16 fp16 MFMAs each followed by
- *      valu_per_mfma (even, 0..12) independent packed-fp16 FMAs; FLOPs = 32768 * 8 * iters * 4 * CUs * waves_per_simd.
- *      How much VALU work per MFMA the GEMM loops can hide. random_operands = 0: sparse constant operands (the issue
- *      rate alone); 1: pseudo-random fp16 operands, distinct per lane and accumulator (the rate the matrix cores hold
- *      on real data, whose power draw sets the clock). sink: a live 4-byte buffer the kernel may write. */
-int p0k_mfma_valu_probe(p0k_ctx *ctx, int valu_per_mfma, int waves_per_simd, int iters, int random_operands, float *sink);
-/*      the LDS read ceiling (no counterpart in the reference): one workgroup of `waves` (4, 8 or 16) waves per CU, each
- *      lane `iters` x 16 conflict-free 16-byte LDS reads (the GEMM loops' fragment read); bytes per CU =
- *      waves * 16384 * iters. clk: a live buffer of 32 * waves * CUs bytes that receives, per wave (workgroup-major),
- *      the shader clock and the 100 MHz reference clock before and after its loop (uint64 each, in that order:
- *      clock start, clock end, reference start, reference end). */
-int p0k_lds_read_probe(p0k_ctx *ctx, int waves, int iters, uint64_t *clk);
 
 /* ---- weight encoders on the host CPU (src/convert/encode.js:56-98): fp32 [rows][K] -> FORMAT.md bytes.
  *      out holds p0k_tensor_bytes(enc, rows, K) bytes; deq (optional) receives the fp32 dequantised weights. */

@@ -17,9 +17,11 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libp0k.so")
 ADDON = os.path.join(PKG, "node", "p0k.node")
+PROBE_SRC = os.path.join(PKG, "probe", "p0k_probe.hip")
+PROBE_LIB = os.path.join(PKG, "probe", "libp0k_probe.so")   # the benchmark's measurement kernels (bench.py only)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["p0k_gemm_mfma.hip", "p0k_gemm_dma.hip", "p0k_gemv.hip", "p0k_rowstats.hip", "p0k_stats.hip", "p0k_attention.hip", "p0k_probe.hip", "p0k_runtime.cpp", "p0k_check.cpp", "p0k_pack.cpp"]
+SOURCES = ["p0k_gemm_mfma.hip", "p0k_gemm_dma.hip", "p0k_gemv.hip", "p0k_rowstats.hip", "p0k_stats.hip", "p0k_attention.hip", "p0k_runtime.cpp", "p0k_check.cpp", "p0k_pack.cpp"]
 HIP_FLAGS = [
     "-x", "hip", "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
     # packed fp32 instructions stay off: ordinary float code only (v_pk_*_f32 are never emitted)
@@ -48,7 +50,18 @@ def build_lib(verbose=False):
             if verbose and out.strip():
                 print(out)
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB] + objs)
+    build_probe()
     return LIB
+
+
+def build_probe():
+    """libp0k_probe.so: the benchmark's HBM / matrix-core / LDS ceiling kernels and its launch gate, linked against
+    libp0k.so (the probes enqueue on a context's stream); not part of the product library."""
+    o = os.path.join(OBJ, "p0k_probe.o")
+    _run([HIPCC] + HIP_FLAGS + ["-c", PROBE_SRC, "-o", o])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", PROBE_LIB, o, "-L" + PKG, "-lp0k",
+          "-Wl,-rpath,$ORIGIN/.."])
+    return PROBE_LIB
 
 
 def build_addon():

@@ -52,11 +52,4 @@ hipError_t launch_pixstats(const void *x, uint32_t V, uint32_t C, float eps, flo
 hipError_t launch_gn_partial(const void *x, uint32_t pix, uint32_t C, float *part, uint32_t wg_off, hipStream_t s);
 hipError_t launch_gn_finalize(const float *part, uint32_t nwg, uint32_t C, float eps, const float *gamma,
                               const float *beta, float *ab, hipStream_t s);
-// the HBM read ceiling probe: reads bytes / 16 16-byte words of buf with `blocks` 512-thread workgroups
-hipError_t launch_stream_read(const void *buf, uint64_t bytes, uint32_t *sink, unsigned blocks, unsigned threads, hipStream_t s);
-// the MFMA / VALU issue probe: `blocks` 256-thread workgroups, `iters` iterations of 8 MFMAs + 8 * valu_per_mfma VALU
-hipError_t launch_mfma_valu(int valu_per_mfma, int random_operands, unsigned blocks, int iters, float *sink, hipStream_t s);
-// the LDS read probe: `blocks` workgroups of `waves` (4, 8, 16) waves, `iters` iterations of 16 ds_read_b128 per lane;
-// clk: 4 uint64 per wave (shader clock and 100 MHz clock before and after the loop)
-hipError_t launch_lds_read(int waves, unsigned blocks, int iters, uint64_t *clk, hipStream_t s);
 }  // namespace p0k

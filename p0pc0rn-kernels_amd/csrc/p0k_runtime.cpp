@@ -37,6 +37,7 @@ int hip_err(hipError_t e, const char *what) {
 struct PooledBuf { void *ptr; uint64_t seq; };
 
 int scratch_setup(int device, hipStream_t s);   // the allocation-free gemm's per-device array (below)
+void scratch_release(int device, const void *owner);
 
 }  // namespace
 
@@ -63,9 +64,14 @@ struct p0k_ctx {
   uint64_t ws_x_bytes = 0;
   // 256 zero bytes: the padding taps of the load-to-LDS conv3 gather read them
   void *ws_zero = nullptr;
-  // workspaces replaced by larger ones: a graph captured earlier may still address them, so they are freed only
-  // with the context
+  // workspaces replaced by larger ones while a graph captured after their allocation may still address them: freed
+  // only with the context. graph_epoch counts the graphs captured on the stream; a workspace allocated in the current
+  // epoch is in no graph and is freed as soon as it is replaced. Workspaces grow to powers of two, so the retired
+  // ones add up to less than the live one.
   std::vector<void *> ws_retired;
+  uint64_t graph_epoch = 0, ws_part_epoch = 0, ws_x_epoch = 0;
+  // this context called p0k_gemm_noalloc and holds its device's scratch array until it is destroyed
+  bool owns_scratch = false;
   // CU count of the device and the P0K_* tuning switches, read at creation and by p0k_ctx_reload_env
   p0k::Tuning tune;
 };
@@ -116,6 +122,7 @@ void p0k_ctx_destroy(p0k_ctx *c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
+  if (c->owns_scratch) scratch_release(c->device, c);
   for (auto &kv : c->live) (void)hipFree(kv.first);
   for (auto &kv : c->pool)
     for (auto &b : kv.second) (void)hipFree(b.ptr);
@@ -136,6 +143,8 @@ int p0k_ctx_reload_env(p0k_ctx *c) {
 }
 
 int p0k_ctx_cus(p0k_ctx *c) { return c ? (int)c->tune.cus : 0; }
+
+void *p0k_ctx_stream(p0k_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 int p0k_device_info_get(p0k_ctx *c, p0k_device_info *out) {
   if (!c || !out) return set_err(P0K_E_ARG, "device_info: NULL argument");
@@ -321,6 +330,21 @@ int p0k_gemm_check(const p0k_gemm_args *a) {
 
 double p0k_gemm_flops(const p0k_gemm_args *a) { return a ? 2.0 * a->M * a->N * a->K : 0.0; }
 
+int p0k_gemm_plan(p0k_ctx *c, const p0k_gemm_args *a, p0k_tile *out) {
+  if (!c) return set_err(P0K_E_ARG, "gemm_plan: NULL context");
+  p0k::Tuning tune;
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    tune = c->tune;
+  }
+  std::string err;
+  p0k::Plan plan;
+  int r = p0k::prepare_gemm(a, nullptr, &plan, &err, tune);
+  if (r) return set_err(r, err);
+  if (out) { out->bm = plan.bm; out->bn = plan.bn; out->kernel = plan.kernel; }
+  return P0K_OK;
+}
+
 int p0k_select_tile(const p0k_gemm_args *a, p0k_tile *out) {
   std::string err;
   p0k::Plan plan;
@@ -341,8 +365,11 @@ static int check_operand(p0k_ctx *c, const void *buf, uint64_t size, const char 
   return P0K_OK;
 }
 
-// grow a workspace of the context to `need` bytes (not while the stream is being captured into a graph)
-static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t need, const char *what) {
+// grow a workspace of the context to at least `need` bytes, rounded up to a power of two (not while the stream is
+// being captured into a graph). The buffer it replaces is freed after the stream has drained when no graph was
+// captured since it was allocated; otherwise it is kept until the context goes, since replaying such a graph still
+// addresses it.
+static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t *epoch, uint64_t need, const char *what) {
   std::lock_guard<std::mutex> lk(c->mu);
   if (need <= *bytes) return P0K_OK;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -350,14 +377,31 @@ static int grow_ws(p0k_ctx *c, void **buf, uint64_t *bytes, uint64_t need, const
   if (cs != hipStreamCaptureStatusNone)
     return set_err(P0K_E_ARG, std::string("gemm: the ") + what + " workspace must grow (" + std::to_string(need) +
                                   " bytes): make one call of this shape before capturing a graph");
+  uint64_t size = 256;
+  while (size < need) size <<= 1;
+  void *old = *buf;
+  if (old && *epoch == c->graph_epoch) {        // in no graph: free it first, so its memory can serve the new one
+    HIPCHK(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    HIPCHK(hipFree(old), "hipFree");
+    old = nullptr;
+    *buf = nullptr;
+    *bytes = 0;
+  }
   void *nb = nullptr;
-  hipError_t me = hipMalloc(&nb, need);
-  if (me != hipSuccess) return set_err(P0K_E_NOMEM, std::string("gemm: ") + what + " workspace of " + std::to_string(need) + " bytes");
-  // the old workspace stays allocated until the context is destroyed: a graph captured before this call still
-  // addresses it, and replaying that graph must not touch freed memory
-  if (*buf) c->ws_retired.push_back(*buf);
+  hipError_t me = hipMalloc(&nb, size);
+  if (me != hipSuccess) return set_err(P0K_E_NOMEM, std::string("gemm: ") + what + " workspace of " + std::to_string(size) + " bytes");
+  if (old) c->ws_retired.push_back(old);
   *buf = nb;
-  *bytes = need;
+  *bytes = size;
+  *epoch = c->graph_epoch;
+  return P0K_OK;
+}
+
+int p0k_ctx_workspace_stats(p0k_ctx *c, uint64_t *live_bytes, uint64_t *retired_buffers) {
+  if (!c) return set_err(P0K_E_ARG, "workspace_stats: NULL context");
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (live_bytes) *live_bytes = c->ws_part_bytes + c->ws_x_bytes;
+  if (retired_buffers) *retired_buffers = c->ws_retired.size();
   return P0K_OK;
 }
 
@@ -378,6 +422,7 @@ namespace {
 constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 uint8_t *g_scratch_ptr[MAX_DEVICES];
+const void *g_scratch_owner[MAX_DEVICES];   // the context whose p0k_gemm_noalloc calls use the array (one at a time)
 
 __global__ void k_zero_words(uint32_t *p, uint32_t n) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
@@ -398,6 +443,10 @@ int scratch_setup(int device, hipStream_t s) {
   g_scratch_ptr[device] = (uint8_t *)ptr;
   return P0K_OK;
 }
+void scratch_release(int device, const void *owner) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (device >= 0 && device < MAX_DEVICES && g_scratch_owner[device] == owner) g_scratch_owner[device] = nullptr;
+}
 }  // namespace
 
 // Where one call's workspaces come from: the context's buffers, grown on demand (p0k_gemm), or the device's scratch
@@ -414,7 +463,7 @@ struct WsSource {
       *out = (float *)(scratch + SCRATCH_WS);
       return P0K_OK;
     }
-    if (int r = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, need, "decode")) return r;
+    if (int r = grow_ws(c, (void **)&c->ws_part, &c->ws_part_bytes, &c->ws_part_epoch, need, "decode")) return r;
     *out = c->ws_part;
     return P0K_OK;
   }
@@ -426,7 +475,7 @@ struct WsSource {
       *out = scratch + SCRATCH_WS;
       return P0K_OK;
     }
-    if (int r = grow_ws(c, &c->ws_x, &c->ws_x_bytes, need, "prologue")) return r;
+    if (int r = grow_ws(c, &c->ws_x, &c->ws_x_bytes, &c->ws_x_epoch, need, "prologue")) return r;
     *out = c->ws_x;
     return P0K_OK;
   }
@@ -473,7 +522,7 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
       if (int rr = ws.part(need, &part)) return rr;
     }
     e = p0k::launch_gemv(p, plan.we, plan.xm, part, ws.counters(), plan.S, plan.KS, c->stream, plan.kernel == p0k::K_GEMV_MF,
-                          c->tune.gemv_mq4, plan.mx, plan.narrow);
+                          tune.gemv_mq4, plan.mx, plan.narrow);
   } else if (plan.kernel == p0k::K_MFMA_DMA && plan.xm == P0K_X_CONV3) {
     p.Z = (const uint8_t *)ws.zero();
     if (p.flags & p0k::F_PN) {
@@ -514,8 +563,18 @@ int p0k_gemm_noalloc(p0k_ctx *c, const p0k_gemm_args *a) {
   if (!c) return set_err(P0K_E_ARG, "gemm_noalloc: NULL context");
   uint8_t *sp;
   {
+    // the first context to call takes the device's array and keeps it until it is destroyed: calls of another
+    // context (another stream) could overlap with its calls on the GPU and corrupt each other's partials and
+    // counters, so they are refused
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     sp = (c->device >= 0 && c->device < MAX_DEVICES) ? g_scratch_ptr[c->device] : nullptr;
+    if (sp) {
+      if (g_scratch_owner[c->device] && g_scratch_owner[c->device] != c)
+        return set_err(P0K_E_ARG, "gemm_noalloc: the scratch array of device " + std::to_string(c->device) +
+                                      " is held by another live context (one context per device may use it)");
+      g_scratch_owner[c->device] = c;
+      c->owns_scratch = true;
+    }
   }
   if (!sp) return set_err(P0K_E_UNSUPPORTED, "gemm_noalloc: the scratch array of this device is not set up");
   return gemm_run(c, a, WsSource{c, sp});
@@ -599,42 +658,6 @@ int p0k_attention(p0k_ctx *c, const p0k_attn_args *a) {
   return P0K_OK;
 }
 
-int p0k_stream_read_probe(p0k_ctx *c, const void *buf, uint64_t bytes, uint32_t *sink, uint32_t blocks, uint32_t threads) {
-  if (!c) return set_err(P0K_E_ARG, "stream_read_probe: NULL context");
-  int r;
-  if ((r = check_live(c, buf, bytes, "stream_read_probe", "buf")) || (r = check_live(c, sink, 4, "stream_read_probe", "sink")))
-    return r;
-  if (((uintptr_t)buf & 15u) != 0) return set_err(P0K_E_ARG, "stream_read_probe: buf must be 16-byte aligned");
-  if (threads != 256 && threads != 512) return set_err(P0K_E_ARG, "stream_read_probe: threads must be 256 or 512");
-  if (bytes >= (1ull << 32)) return set_err(P0K_E_ARG, "stream_read_probe: bytes must be below 4 GiB");
-  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_stream_read(buf, bytes, sink, blocks ? blocks : c->tune.cus * 7u / 8u, threads, c->stream);
-  if (e != hipSuccess) return hip_err(e, "stream_read_probe launch");
-  return P0K_OK;
-}
-
-int p0k_mfma_valu_probe(p0k_ctx *c, int valu_per_mfma, int waves_per_simd, int iters, int random_operands, float *sink) {
-  if (!c) return set_err(P0K_E_ARG, "mfma_valu_probe: NULL context");
-  if (waves_per_simd < 1 || waves_per_simd > 2 || iters < 1 || valu_per_mfma < 0 || valu_per_mfma > 12 || valu_per_mfma % 2)
-    return set_err(P0K_E_ARG, "mfma_valu_probe: waves_per_simd 1 or 2, iters > 0, valu_per_mfma even in 0..12");
-  if (int r = check_live(c, sink, 4, "mfma_valu_probe", "sink")) return r;
-  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_mfma_valu(valu_per_mfma, random_operands != 0, c->tune.cus * (unsigned)waves_per_simd, iters, sink, c->stream);
-  if (e != hipSuccess) return hip_err(e, "mfma_valu_probe launch");
-  return P0K_OK;
-}
-
-int p0k_lds_read_probe(p0k_ctx *c, int waves, int iters, uint64_t *clk) {
-  if (!c) return set_err(P0K_E_ARG, "lds_read_probe: NULL context");
-  if ((waves != 4 && waves != 8 && waves != 16) || iters < 1)
-    return set_err(P0K_E_ARG, "lds_read_probe: waves 4, 8 or 16, iters > 0");
-  if (int r = check_live(c, clk, (uint64_t)32 * (uint64_t)waves * c->tune.cus, "lds_read_probe", "clk")) return r;
-  HIPCHK(hipSetDevice(c->device), "hipSetDevice");
-  hipError_t e = p0k::launch_lds_read(waves, c->tune.cus, iters, clk, c->stream);
-  if (e != hipSuccess) return hip_err(e, "lds_read_probe launch");
-  return P0K_OK;
-}
-
 uint64_t p0k_gn_part_bytes(uint32_t pix) { return (uint64_t)((pix + 63) / 64) * 512; }
 
 static int gn_run(p0k_ctx *c, const p0k_gn_args *a, int what, uint32_t *nwg_out) {
@@ -683,6 +706,10 @@ int p0k_graph_end(p0k_ctx *c, p0k_graph **out) {
   *out = nullptr;
   hipGraph_t g = nullptr;
   HIPCHK(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->graph_epoch++;                  // the workspaces now in use may be addressed by this graph
+  }
   hipGraphExec_t ex = nullptr;
   hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
   if (e != hipSuccess) { (void)hipGraphDestroy(g); return hip_err(e, "hipGraphInstantiate"); }

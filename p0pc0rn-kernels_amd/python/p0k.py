@@ -130,8 +130,8 @@ class DeviceInfo(C.Structure):
 
 EXPORTS = [
     "p0k_abi_version", "p0k_last_error", "p0k_ctx_create", "p0k_ctx_destroy", "p0k_device_info_get", "p0k_alloc",
-    "p0k_ctx_reload_env", "p0k_ctx_cus", "p0k_gemm_noalloc", "p0k_gemm_noalloc_scratch_bytes", "p0k_stream_read_probe",
-    "p0k_mfma_valu_probe", "p0k_lds_read_probe",
+    "p0k_ctx_reload_env", "p0k_ctx_cus", "p0k_gemm_noalloc", "p0k_gemm_noalloc_scratch_bytes", "p0k_ctx_stream",
+    "p0k_ctx_workspace_stats", "p0k_gemm_plan",
     "p0k_free", "p0k_drain_pool", "p0k_pool_stats_get", "p0k_upload", "p0k_download", "p0k_copy", "p0k_sync",
     "p0k_gemm_check", "p0k_gemm", "p0k_gemm_flops", "p0k_select_tile", "p0k_rowstats_check", "p0k_rowstats",
     "p0k_attention_check", "p0k_attention", "p0k_attention_flops",
@@ -157,8 +157,9 @@ def lib():
             "p0k_ctx_create": ([I, C.POINTER(P)], I), "p0k_ctx_destroy": ([P], None),
             "p0k_ctx_reload_env": ([P], I), "p0k_ctx_cus": ([P], I),
             "p0k_gemm_noalloc": ([P, C.POINTER(GemmArgs)], I), "p0k_gemm_noalloc_scratch_bytes": ([], U64),
-            "p0k_stream_read_probe": ([P, P, U64, P, C.c_uint32, C.c_uint32], I),
-            "p0k_mfma_valu_probe": ([P, I, I, I, I, P], I), "p0k_lds_read_probe": ([P, I, I, P], I),
+            "p0k_ctx_stream": ([P], P),
+            "p0k_ctx_workspace_stats": ([P, C.POINTER(U64), C.POINTER(U64)], I),
+            "p0k_gemm_plan": ([P, C.POINTER(GemmArgs), C.POINTER(Tile)], I),
             "p0k_device_info_get": ([P, C.POINTER(DeviceInfo)], I),
             "p0k_alloc": ([P, U64, C.POINTER(P)], I), "p0k_free": ([P, P], I), "p0k_drain_pool": ([P], I),
             "p0k_pool_stats_get": ([P, C.POINTER(PoolStats)], I),
@@ -379,18 +380,18 @@ class Device:
         _chk(lib().p0k_gemm_noalloc(self.ctx, C.byref(s)))
         return 2 * a["M"] * a["N"] * a["K"]
 
-    def stream_read_probe(self, buf, nbytes, sink, blocks=0, threads=512):
-        """the HBM read ceiling kernel: read nbytes of buf, nothing stored"""
-        _chk(lib().p0k_stream_read_probe(self.ctx, buf.ptr, int(nbytes), sink.ptr, int(blocks), int(threads)))
+    def select_tile(self, a):
+        """the kernel and tile p0k_gemm uses for these arguments on this context (its CU count and switches)"""
+        s = gemm_args(a, lambda b: (b.ptr, b.size) if isinstance(b, Buffer) else numpy_resolve(b))
+        self._sync_env()
+        t = Tile()
+        _chk(lib().p0k_gemm_plan(self.ctx, C.byref(s), C.byref(t)))
+        return _tile_dict(t)
 
-    def mfma_valu_probe(self, valu_per_mfma, waves_per_simd, iters, sink, random_operands=False):
-        """the matrix-core issue ceiling kernel (see include/p0k.h)"""
-        _chk(lib().p0k_mfma_valu_probe(self.ctx, int(valu_per_mfma), int(waves_per_simd), int(iters),
-                                       int(bool(random_operands)), sink.ptr))
-
-    def lds_read_probe(self, waves, iters, clk):
-        """the LDS read ceiling kernel (see include/p0k.h); clk: a buffer of 32 * waves * CUs bytes"""
-        _chk(lib().p0k_lds_read_probe(self.ctx, int(waves), int(iters), clk.ptr))
+    def workspace_stats(self):
+        live, retired = C.c_uint64(), C.c_uint64()
+        _chk(lib().p0k_ctx_workspace_stats(self.ctx, C.byref(live), C.byref(retired)))
+        return {"live_bytes": live.value, "retired_buffers": retired.value}
 
     def gemm_raw(self, s):
         _chk(lib().p0k_gemm(self.ctx, C.byref(s)))
@@ -517,4 +518,8 @@ def select_tile(a):
     s = gemm_args(a, lambda b: (b.ptr, b.size) if isinstance(b, Buffer) else numpy_resolve(b))
     t = Tile()
     _chk(lib().p0k_select_tile(C.byref(s), C.byref(t)))
+    return _tile_dict(t)
+
+
+def _tile_dict(t):
     return {"BM": t.bm, "BN": t.bn, "kernel": {1: "gemv", 2: "gemv_mfma", 3: "mfma_dma"}.get(t.kernel, "mfma")}

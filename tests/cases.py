@@ -55,6 +55,7 @@ class Case:
 
     def __init__(self, spec, bufs, out="y"):
         self.spec, self.bufs, self.out = spec, bufs, out
+        self.kernel = None
 
     def args(self, lookup):
         def sub(v):
@@ -74,7 +75,10 @@ class Case:
         a = self.args(lambda n: h[n])
         if weights is None:
             import p0k
-            weights = oracle.CPU_WEIGHTS if p0k.select_tile(a)["kernel"].startswith("gemv") else oracle.KERNEL_WEIGHTS
+            # the kernel the last run_device call planned on its device (its CU count); without one, the
+            # context-free plan for a 256-CU device
+            kern = self.kernel or p0k.select_tile(a)["kernel"]
+            weights = oracle.CPU_WEIGHTS if kern.startswith("gemv") else oracle.KERNEL_WEIGHTS
         oracle.gemm(a, m0, m1, weights)
         return h[self.out]
 
@@ -82,6 +86,7 @@ class Case:
         """upload every buffer, run, read the output back (bytes -> dtype of the host array)."""
         d = {k: dev.upload(v) for k, v in self.bufs.items()}
         try:
+            self.kernel = dev.select_tile(self.args(lambda n: d[n]))["kernel"]
             dev.gemm(self.args(lambda n: d[n]))
             out = self.bufs[self.out]
             return dev.read(d[self.out], out.dtype, out.size)

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), f"{n} is declared in include/p0k.h but not exported"
     assert set(names) == set(p0k.EXPORTS)
-    assert L.p0k_abi_version() == 3
+    assert L.p0k_abi_version() == 4
 
 
 def test_struct_layout_matches():

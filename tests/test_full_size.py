@@ -63,7 +63,7 @@ def test_decode_q4_swiglu_full(dev, M, path, monkeypatch):
         monkeypatch.setenv("P0K_GEMV_MQ4", "0")
     banner(f"full-size decode M={M} path={path}")
     c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=28672, K=4096, seed=101, wscale=0.02)
-    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    t = dev.select_tile(c.args(lambda n: c.bufs[n]))
     assert t["kernel"] == ("gemv" if path in ("stream", "mx") else "gemv_mfma")
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"decode M={M}")
@@ -96,7 +96,7 @@ def test_prefill_full(dev, name):
     kw = FULL[name]
     banner(f"full-size {name}")
     c = make_case(seed=102, **kw)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
     got = c.run_device(dev)
     M = kw["M"]
     ranges = [(0, 8), (M // 2 - 3, M // 2 + 5), (M - 8, M)]

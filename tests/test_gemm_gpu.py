@@ -102,7 +102,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     K = 256
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
-    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
     assert kern == ("gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
@@ -110,7 +110,7 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     if kern == "mfma_dma":
         # the register-staged MFMA kernel on the same call
         monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
-        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma"
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma"
         got = c.run_device(dev)
         assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M} register-staged")
 
@@ -139,7 +139,7 @@ def test_matrix_core_decode_offsets(dev, kw, path, monkeypatch):
     monkeypatch.setenv("P0K_GEMV_MX", "0" if path == "mq4" else "16")
     banner(f"matrix-core decode {path} {kw}")
     c = make_case(seed=31, **kw)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv_mfma" if path == "mq4" else "gemv")
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv_mfma" if path == "mq4" else "gemv")
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"decode {kw}")
 
@@ -153,7 +153,7 @@ def test_matrix_core_stream_long_k(dev, M, K, slices, monkeypatch):
         monkeypatch.setenv("P0K_GEMV_SLICES", str(slices))
     banner(f"matrix-core stream M={M} K={K} slices={slices}")
     c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=512, K=K, seed=41)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), what=f"stream M={M} K={K}")
 
@@ -216,7 +216,7 @@ def test_narrow_decode_items(dev, epi, M, N, K, narrow, monkeypatch):
     monkeypatch.setenv("P0K_GEMV_NARROW", "1" if narrow else "0")
     banner(f"narrow={narrow} {epi} M={M} N={N} K={K}")
     c = make_case(enc="q4g32a.t64", epi=epi, M=M, N=N, K=K, seed=91)
-    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    t = dev.select_tile(c.args(lambda n: c.bufs[n]))
     assert t["kernel"] == ("gemv" if M <= 4 else "gemv_mfma") and t["BN"] == (64 if narrow else 128)
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"{epi} M={M} N={N}")
@@ -238,7 +238,7 @@ def test_narrow_matrix_core_decode(dev, enc, epi, M, N, K, mq4, narrow, monkeypa
     monkeypatch.setenv("P0K_GEMV_MQ4", mq4)
     banner(f"narrow={narrow} {enc} {epi} M={M} N={N} K={K} mq4={mq4}")
     c = make_case(enc=enc, epi=epi, M=M, N=N, K=K, seed=93)
-    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    t = dev.select_tile(c.args(lambda n: c.bufs[n]))
     assert t["kernel"] == "gemv_mfma" and t["BN"] == (64 if narrow else 128)
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16,
@@ -360,7 +360,7 @@ def test_conv3_chunks_and_ring_bit_identical(dev, dims):
 @pytest.mark.parametrize("C", [32, 128])
 def test_conv3_pixelnorm(dev, C):
     c = make_conv3_case(C=C, pn=True)
-    assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("mfma_dma" if C % 64 == 0 else "mfma")
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("mfma_dma" if C % 64 == 0 else "mfma")
     assert_close(c.run_device(dev), c.run_oracle(), what=f"conv3 pn C={C}")
 
 
@@ -375,7 +375,7 @@ def test_conv3_gather_every_tile(dev, enc, pn, monkeypatch):
     for t in MFMA_TILES:
         banner(f"conv3 gather tile {t} enc {enc} pn {pn}")
         monkeypatch.setenv("P0K_MFMA_TILE", t)
-        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
         got = c.run_device(dev)
         assert_close(got, want, what=f"conv3 gather tile {t}")
         outs.append(got)
@@ -452,14 +452,14 @@ def test_every_mfma_tile_matches_oracle(dev, kw, kernel, monkeypatch):
     want = c.run_oracle()
     if kernel == "mfma":
         monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
-    elif p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] != "mfma_dma":
+    elif dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] != "mfma_dma":
         pytest.skip("the call does not qualify for the load-to-LDS kernel")
     outs = []
     for t in MFMA_TILES:
         banner(f"tile {t} {kernel} {kw}")
         monkeypatch.setenv("P0K_MFMA_TILE", t)
         a = c.args(lambda n: c.bufs[n])
-        assert p0k.select_tile(a)["BM"] == int(t.split("x")[0]) and p0k.select_tile(a)["kernel"] == kernel
+        assert dev.select_tile(a)["BM"] == int(t.split("x")[0]) and dev.select_tile(a)["kernel"] == kernel
         got = c.run_device(dev)
         assert_close(got, want, fp16=want.dtype == np.uint16, what=f"tile {t} {kernel}")
         outs.append(got)
@@ -519,7 +519,7 @@ def test_q4_256x128_four_wave_grid(dev, monkeypatch):
     outs = {}
     for t in ("256x128", "256x256"):
         monkeypatch.setenv("P0K_MFMA_TILE", t)
-        sel = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+        sel = dev.select_tile(c.args(lambda n: c.bufs[n]))
         assert sel["kernel"] == "mfma_dma" and sel["BM"] == 256 and sel["BN"] == int(t.split("x")[1])
         outs[t] = c.run_device(dev)
     assert np.array_equal(outs["256x128"], outs["256x256"])
@@ -557,7 +557,7 @@ def test_graph_survives_workspace_growth(dev):
     small = make_case(enc="q4g32a.t64", epi="swiglu", M=1, N=1024, K=4096, seed=71, wscale=0.02)
     big = make_case(enc="q4g32a.t64", epi="swiglu", M=8, N=8192, K=4096, seed=72, wscale=0.02)
     for c in (small, big):
-        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"].startswith("gemv")
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"].startswith("gemv")
     d = {k: dev.upload(v) for k, v in small.bufs.items()}
     db = {k: dev.upload(v) for k, v in big.bufs.items()}
     try:
@@ -586,61 +586,6 @@ def test_graph_survives_workspace_growth(dev):
             dev.free(b)
 
 
-def test_stream_read_probe(dev):
-    """the HBM read-ceiling probe runs on a live buffer and refuses foreign or misaligned ranges"""
-    b, sink = dev.buffer(1 << 20), dev.buffer(16)
-    try:
-        dev.stream_read_probe(b, 1 << 20, sink)
-        dev.stream_read_probe(b, 1 << 20, sink, blocks=512, threads=256)
-        dev.done()
-        with pytest.raises(p0k.P0kError, match="threads"):
-            dev.stream_read_probe(b, 1 << 20, sink, threads=1024)
-        with pytest.raises(p0k.P0kError, match="size exceeds"):
-            dev.stream_read_probe(b, 2 << 20, sink)
-        with pytest.raises(p0k.P0kError):
-            p0k._chk(p0k.lib().p0k_stream_read_probe(dev.ctx, b.ptr + 4, 1024, sink.ptr, 0, 512))
-    finally:
-        dev.free(b)
-        dev.free(sink)
-
-
-def test_lds_read_probe(dev):
-    """the LDS read probe runs, writes ordered clock pairs for every wave, and refuses out-of-range settings"""
-    cus = dev.cus()
-    clk = dev.buffer(32 * 16 * cus)
-    try:
-        for waves in (4, 8, 16):
-            dev.lds_read_probe(waves, 8, clk)
-            dev.done()
-            t = dev.read(clk, np.uint64, 4 * waves * cus).reshape(-1, 4)
-            assert np.all(t[:, 1] > t[:, 0]) and np.all(t[:, 3] >= t[:, 2]), f"waves {waves}: clocks out of order"
-        with pytest.raises(p0k.P0kError, match="waves 4, 8 or 16"):
-            dev.lds_read_probe(6, 8, clk)
-        small = dev.buffer(32 * 4)
-        try:
-            with pytest.raises(p0k.P0kError):
-                dev.lds_read_probe(4, 8, small)                  # smaller than 32 * waves * CUs bytes
-        finally:
-            dev.free(small)
-    finally:
-        dev.free(clk)
-
-
-def test_mfma_valu_probe(dev):
-    """the matrix-core issue probe runs and refuses out-of-range settings"""
-    sink = dev.buffer(16)
-    try:
-        dev.mfma_valu_probe(4, 2, 3, sink)
-        dev.mfma_valu_probe(0, 1, 3, sink, random_operands=True)
-        dev.done()
-        with pytest.raises(p0k.P0kError, match="waves_per_simd"):
-            dev.mfma_valu_probe(3, 2, 3, sink)
-        with pytest.raises(p0k.P0kError, match="waves_per_simd"):
-            dev.mfma_valu_probe(4, 3, 3, sink)
-    finally:
-        dev.free(sink)
-
-
 @pytest.mark.parametrize("kernel", ["mfma_dma", "mfma"])
 def test_heads_tiles_past_n_write_nothing(dev, kernel, monkeypatch):
     """A heads call whose last column tile reaches past N (3 heads of 128 in tiles 256 wide) must not write the
@@ -659,7 +604,7 @@ def test_heads_tiles_past_n_write_nothing(dev, kernel, monkeypatch):
         try:
             a = c.args(lambda n: d[n])
             a["y"]["size"] = need
-            assert p0k.select_tile(a)["kernel"] == kernel
+            assert dev.select_tile(a)["kernel"] == kernel
             dev.gemm(a)
             out = dev.read(d["y"], np.uint8)
         finally:
@@ -667,3 +612,46 @@ def test_heads_tiles_past_n_write_nothing(dev, kernel, monkeypatch):
                 dev.free(b)
         assert np.array_equal(out[need:need + guard.size], guard), f"{kernel} tile {t}: wrote past the heads output"
         assert_close(out[:need].view(np.uint16), want, what=f"heads past N {kernel} tile {t}")
+
+
+def test_workspace_growth_stays_bounded(dev):
+    """rms X' workspaces for rising M: each grows to a power of two and the one it replaces is freed when no graph was
+    captured since it was allocated (at most the first one of the series can predate a graph of an earlier test), so
+    the workspaces grow by less than twice the largest need; after a graph capture the replaced one is kept (the graph
+    may replay it) and the graph still replays correctly"""
+    K = 512
+    live0 = dev.workspace_stats()
+    for M in (40, 80, 160, 320, 640, 1280):
+        c = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=M, N=128, K=K, seed=90 + M)
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
+        got = c.run_device(dev)
+        assert_close(got, c.run_oracle(), what=f"rms M={M}")
+        st = dev.workspace_stats()
+        assert st["retired_buffers"] <= live0["retired_buffers"] + 1, f"M={M}: workspaces retired without a graph"
+        assert st["live_bytes"] <= live0["live_bytes"] + 2 * 1280 * K * 2
+    # capture a graph on the current workspace, then grow past it: the old one must be kept and the graph must replay
+    c = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=64, N=128, K=K, seed=97)
+    d = {k: dev.upload(v) for k, v in c.bufs.items()}
+    try:
+        a = c.args(lambda n: d[n])
+        dev.gemm(a)
+        dev.done()
+        dev.graph_begin()
+        try:
+            dev.gemm(a)
+        finally:
+            g = dev.graph_end()
+        before = dev.workspace_stats()
+        Mbig = (before["live_bytes"] // (2 * K) + 64 + 63) // 64 * 64       # an X' larger than every workspace held
+        big = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=Mbig, N=128, K=K, seed=98)
+        print(f"[p0k-test] workspace growth past a graph: M={Mbig}", flush=True)
+        big.run_device(dev)
+        assert dev.workspace_stats()["retired_buffers"] == before["retired_buffers"] + 1
+        dev.upload(np.zeros_like(c.bufs["y"]), d["y"])
+        dev.graph_launch(g)
+        dev.done()
+        dev.graph_destroy(g)
+        assert_close(dev.read(d["y"], np.uint16, c.bufs["y"].size), c.run_oracle(), what="graph replay after growth")
+    finally:
+        for b in d.values():
+            dev.free(b)

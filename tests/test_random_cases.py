@@ -63,7 +63,7 @@ CASES = _cases()
                                            for i, k in enumerate(CASES)])
 def test_random_case_matches_oracle(dev, kw):
     c = make_case(**kw)
-    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
     print(f"[p0k-test] random case {kw} kernel={kern}", flush=True)
     got = c.run_device(dev)
     want = c.run_oracle()
@@ -94,7 +94,7 @@ GLU_CASES = _glu_cases()
                                                for i, k in enumerate(GLU_CASES)])
 def test_random_glu_case_matches_oracle(dev, kw):
     c = make_case(**kw)
-    kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
+    kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
     print(f"[p0k-test] random GLU case {kw} kernel={kern}", flush=True)
     got = c.run_device(dev)
     want = c.run_oracle()
@@ -141,7 +141,7 @@ NARROW_CASES = _narrow_cases()
                                                   for i, k in enumerate(NARROW_CASES)])
 def test_random_narrow_case_matches_oracle(dev, kw):
     c = make_case(**kw)
-    t = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+    t = dev.select_tile(c.args(lambda n: c.bufs[n]))
     assert t["kernel"] == "gemv_mfma" and t["BN"] == 64, t
     print(f"[p0k-test] random narrow case {kw}", flush=True)
     got = c.run_device(dev)

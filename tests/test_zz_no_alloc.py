@@ -38,7 +38,7 @@ def test_noalloc_matches_gemm(dev, name):
     for i, kw in enumerate(PAIRS[name]):
         print(f"[no-alloc] {name} call {i} {kw}", flush=True)
         c = make_case(**kw)
-        kern = p0k.select_tile(c.args(lambda n: c.bufs[n]))
+        kern = dev.select_tile(c.args(lambda n: c.bufs[n]))
         if kw["M"] <= 16:
             assert kern["kernel"].startswith("gemv")
         else:
@@ -53,7 +53,7 @@ def test_noalloc_conv3_pixelnorm(dev):
     for i, (T, H, W) in enumerate([(3, 10, 12), (2, 6, 8)]):
         print(f"[no-alloc] conv3 pn call {i}", flush=True)
         c = make_conv3_case(T=T, H=H, W=W, C=64, N=128, pn=True)
-        assert p0k.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "mfma_dma"
         want = run(dev, c, dev.gemm)
         got = run(dev, c, dev.gemm_noalloc)
         assert np.array_equal(got, want)
@@ -66,3 +66,17 @@ def test_noalloc_refuses_oversized_workspace(dev):
     c = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=M, N=128, K=K, seed=87)
     with pytest.raises(p0k.P0kError, match="scratch array holds"):
         run(dev, c, dev.gemm_noalloc)
+
+
+def test_noalloc_refuses_a_second_context(dev):
+    """the first context to call p0k_gemm_noalloc holds the device's scratch array; another live context on the same
+    device is refused (its stream could overlap the holder's calls), and may take it once the holder is gone"""
+    c = make_case(enc="q4g32a.t64", epi="swiglu", M=2, N=512, K=2048, seed=88, wscale=0.02)
+    run(dev, c, dev.gemm_noalloc)                       # dev holds the array from here on
+    other = p0k.Device(0)
+    try:
+        with pytest.raises(p0k.P0kError, match="held by another live context"):
+            run(other, c, other.gemm_noalloc)
+        assert np.array_equal(run(other, c, other.gemm), run(dev, c, dev.gemm_noalloc))   # plain gemm is unaffected
+    finally:
+        other.close()
