@@ -68,7 +68,7 @@ MALL = 256 << 20
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36000, 28), "decode_q4_swiglu_M1_long": (36000, 28), "decode_q4_swiglu_M4": (36140, 112), "decode_q4_swiglu_M16": (37299, 448),
                "hbm_read_ceiling_73MB": (35851, 0), "prefill_rowstats_rms": (16403, 64),
-               "decode_q4_plain_M1": (18014, 28), "decode_q4_plain_N4096_M1": (5199, 8), "decode_q8_plain_M1": (30285, 28),
+               "decode_q4_plain_M1": (18014, 28), "decode_q4_plain_N4096_M1": (5199, 8), "hbm_read_ceiling_10MB": (5120, 0), "decode_q8_plain_M1": (30285, 28),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
                "dit_qkv_q4_lnmod_heads": (132057, 98304), "dit_up_q4_geglu": (250822, 98304),
@@ -270,16 +270,16 @@ def dit_attn(dev):
                     4.0 * L * L * 128 * H, 4 * H * L * 128 * 2, L, args, [q, k, v, o], kind="attn")
 
 
-def hbm_ceiling(dev, blocks=0, threads=512):
+def hbm_ceiling(dev, blocks=0, threads=512, nbytes=None, name=None):
     """the measured HBM read ceiling for the headline: a plain streaming read (p0kprobe_stream_read, nothing computed or
     stored) of as many bytes as the q4 decode's weights (73,400,320), rotated over the same number of copies; by default
     with the decode GEMV's grid (blocks 0: 7/8 of the CUs, 512 threads)"""
-    nbytes = 28672 // 64 * (4096 // 32) * 1280
+    nbytes = nbytes or 28672 // 64 * (4096 // 32) * 1280
     copies = max(4, -(-(2 * MALL) // nbytes))
     bufs = [dev.buffer(nbytes) for _ in range(copies)]
     sink = dev.buffer(16)
     args = [{"buf": b, "bytes": nbytes, "sink": sink, "blocks": blocks, "threads": threads} for b in bufs]
-    name = "hbm_read_ceiling_73MB" + (f"_{blocks}x{threads}" if blocks else "")
+    name = name or "hbm_read_ceiling_73MB" + (f"_{blocks}x{threads}" if blocks else "")
     return Workload(name, f"plain streaming read of the decode's weight bytes (ceiling probe, grid "
                           f"{blocks or 'GEMV'} x {threads} threads)", "hbm", 0.0,
                     nbytes, 1, args, bufs + [sink], {"weight_copies": copies}, kind="probe")
@@ -298,6 +298,8 @@ BUILDERS = {
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "decode1_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096),
     "decode1_q8": lambda d: decode_q4(d, 1, glu=False, enc="q8g64s.t64"),
+    "hbm_ceiling_proj": lambda d: hbm_ceiling(d, 256, 256, nbytes=4096 // 64 * (4096 // 32) * 1280,
+                                              name="hbm_read_ceiling_10MB"),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,
     "dit_qkv": dit_qkv, "dit_up": dit_up, "conv3": conv3, "dit_attn": dit_attn,
 }

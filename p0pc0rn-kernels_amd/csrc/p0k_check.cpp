@@ -58,6 +58,7 @@ Tuning tuning_from_env(unsigned cus) {
   if (const char *ov = getenv("P0K_GEMV_SLICES")) t.gemv_slices = (unsigned)std::max(0, atoi(ov));
   if (const char *ov = getenv("P0K_GEMV_MX")) t.gemv_mx = (unsigned)std::max(0, atoi(ov));
   if (const char *ov = getenv("P0K_GEMV_NARROW")) t.gemv_narrow = atoi(ov) != 0;
+  if (const char *ov = getenv("P0K_GEMV_SN")) t.gemv_sn = atoi(ov) != 0;
   if (const char *ov = getenv("P0K_MFMA_KERNEL")) t.mfma_reg = strcmp(ov, "reg") == 0;
   if (const char *ov = getenv("P0K_MFMA_TILE")) {
     unsigned tm = 0, tn = 0;
@@ -72,6 +73,17 @@ Tuning tuning_from_env(unsigned cus) {
     if (v == 128 || v == 256) t.attn_bq = v;
   }
   return t;
+}
+
+// Where the short-call decode items are taken: at most about one 16-row item per CU (one and a half at one row), one
+// or two rows, K up to 8192. Measured per call against the planner's other choice (ring kernels, 64-column items or a
+// K split), q4, K 4096 unless stated: plain N 2048 M 1 3.88 vs 6.07 us, M 2 5.35 vs 6.79; N 4096 M 1 4.45 vs 6.17,
+// M 2 6.06 vs 6.89, M 4 7.92 vs 7.35; N 6144 M 1 6.02 vs 6.43, M 2 7.77 vs 7.08; N 14336 M 1 9.71 vs 7.98; N 4096
+// K 8192 M 1 7.81 vs 9.98; K 14336 12.0 vs 11.9; SwiGLU out 4096 (8192 weight rows) M 1 7.91 vs 7.57. (A plain
+// one-launch read of the same 10.5 MB as N 4096 K 4096 takes 4.3-4.5 us: the short calls are latency, not bytes.)
+static bool sn_rule(uint32_t N, uint32_t K, uint32_t M, unsigned cus) {
+  const uint64_t items = (N + 15u) / 16u;
+  return M <= 2 && K <= 8192u && items * 2u <= (uint64_t)cus * (M == 1 ? 3u : 2u);
 }
 
 int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *err, const Tuning &tune) {
@@ -300,11 +312,21 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
         if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
+      // short calls (q4, up to 4 rows, element-wise epilogues): 16-row items, no K split, every load of an item in
+      // flight at once (SHORT_RULE below)
+      const bool sn_ok = we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS && epi != P0K_EPI_ONORMGATE &&
+                         K <= gemv_sn_kmax() && a->wk0 % 32 == 0 && (uint64_t)(M <= 2 ? M : 4) * K * 2 + (uint64_t)(M <= 2 ? M : 4) * (K / 32) * 8 <= 64u * 1024u;
+      if (sn_ok && (tune.gemv_sn == 1 || (tune.gemv_sn < 0 && sn_rule(N, K, M, tune.cus)))) {
+        kernel = K_GEMV_SN;
+        S = 1;
+        KS = K;
+        narrow = false;
+      }
     }
   }
   if (out) *out = p;
   if (plan) {
-    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = narrow ? 64 : 128; plan->mx = mx; plan->narrow = narrow;
+    plan->kernel = kernel; plan->we = we; plan->xm = xm; plan->bm = 16; plan->bn = kernel == K_GEMV_SN ? 16 : narrow ? 64 : 128; plan->mx = mx; plan->narrow = narrow;
     // the load-to-LDS kernel where it applies (P0K_MFMA_KERNEL=reg keeps the register-staged one, for tests)
     if (kernel == K_MFMA && gemm_dma_ok(p, we, xm, wbytes) && !tune.mfma_reg) kernel = plan->kernel = K_MFMA_DMA;
     if (kernel == K_MFMA_DMA) dma_tile(M, N, we, xm == P0K_X_CONV3 ? X_CONV3 : X_F16, tune.cus, &plan->bm, &plan->bn);

@@ -475,6 +475,201 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// Short decode calls (q4, 1..4 rows, element-wise epilogues): items of 16 weight rows, so that even N = 4096 gives one
+// item per CU with no K split. A call of this size is mostly latency (launch, the first bytes' trip from HBM, the
+// finish), and a ring per lane keeps only a few units in flight per CU; here every lane issues all of its weight loads
+// at once (the whole item, 16 rows x K, is in flight on the CU right after the launch), X' is staged in LDS with its
+// per-unit sums while those loads travel, and each lane reduces its units with the same algebraic form as k_gemv. Lane
+// l of a wave owns row l % 16 of the item and unit l / 16 of every round of 4 units; the 8 waves take rounds of 32
+// consecutive units (wave w the units 4 w .. 4 w + 3 of each). The four lanes of a row meet by DPP, the waves in LDS
+// (wave order), and one thread per output element applies the epilogue. With the SwiGLU interleave, rows 0..7 of an
+// item are 8 consecutive gate rows and rows 8..15 the matching up rows.
+constexpr int SN_NT = 512, SN_ROWS = 16;
+template <int XM, int MT, int RND>
+__global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
+  constexpr int UK = 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ri = lane & 15, us = lane >> 4;
+  const bool glu = p.epi == E_SWIGLU;
+  const uint32_t nB = blockIdx.x * (uint32_t)SN_ROWS;
+  const uint32_t wsc = glu ? (ri < 8 ? 2u * ri : 2u * (ri - 8) + 1u) : (uint32_t)ri;
+  const uint32_t r = wrow(p, nB + wsc);
+  const uint32_t nun = p.K / UK;                               // units (32 k) of the call
+  const uint32_t woff = ((r >> 6) * p.wG + (p.wk0 >> 5)) * 1280u + (r & 63u) * 16u;
+  const uint32_t sadj = 1024u - (r & 63u) * 12u;             // code row -> scale word of row r in the record
+  const srsrc wr = stream_rsrc(p.W);
+  // this thread's first chunk of X before the weights (loads return in issue order: issued after them, it would wait
+  // for the whole item's weights before the staging below could start)
+  const uint32_t nb = p.K / 8, nx = MT * nb;                   // 8-k chunks (nx is a multiple of 4: whole lane quads)
+  u32x4 xv0 = (u32x4){0u, 0u, 0u, 0u};
+  if ((uint32_t)tid < nx && (uint32_t)tid / nb < p.M) xv0 = xload8<XM>(p, tid / nb, RowCtx{0, 0, 0}, 8 * (tid % nb));
+  __builtin_amdgcn_sched_barrier(0);
+  // every weight load of this lane (clamped past the last unit: the clamped ones are not reduced)
+  u32x4 code[RND];
+  uint32_t sm[RND];
+#pragma unroll
+  for (int rd = 0; rd < RND; rd++) {
+    uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)us;
+    u = u < nun ? u : nun - 1u;
+    code[rd] = sload128(wr, woff + u * 1280u);
+    sm[rd] = sload32(wr, woff + u * 1280u + sadj);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // X' -> LDS in the pair order of the encoding, and per unit and row the X' sums over the low / high nibble positions
+  extern __shared__ __attribute__((aligned(16))) uint8_t sn_smem[];
+  f16 *sX = (f16 *)sn_smem;                                    // [MT][K]
+  f32x2 *sG = (f32x2 *)(sn_smem + (size_t)MT * p.K * 2);      // [MT][K / 32]
+  for (uint32_t t = tid; t < (nx + 3u) / 4u * 4u; t += SN_NT) {
+    const uint32_t m = t / nb, kq = t - m * nb;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (t == (uint32_t)tid) v = xv0;
+    else if (t < nx && m < p.M) v = xload8<XM>(p, m, RowCtx{0, 0, 0}, 8 * kq);
+    v = xperm<W_Q4>(v);
+    const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+    float lo = __builtin_amdgcn_fdot2(as_h2(v.z), one2, __builtin_amdgcn_fdot2(as_h2(v.x), one2, 0.0f, false), false);
+    float hi = __builtin_amdgcn_fdot2(as_h2(v.w), one2, __builtin_amdgcn_fdot2(as_h2(v.y), one2, 0.0f, false), false);
+    lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0xB1, 0xF, 0xF, false));
+    hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0xB1, 0xF, 0xF, false));
+    lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0x4E, 0xF, 0xF, false));
+    hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0x4E, 0xF, 0xF, false));
+    if (t < nx) {
+      if (kq % 4u == 0u) sG[m * (nb / 4u) + kq / 4u] = (f32x2){lo, hi};
+      *(u32x4 *)(sX + (size_t)m * p.K + 8 * kq) = v;
+    }
+  }
+  __syncthreads();
+
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mag = 0x64006400u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi), "+v"(mag));
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; m++) acc[m] = 0.0f;
+#pragma unroll
+  for (int rd = 0; rd < RND; rd++) {
+    const uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)us;
+    if (u >= nun) break;                                       // (units ascend with rd)
+    const uint32_t wd[4] = {code[rd].x, code[rd].y, code[rd].z, code[rd].w};
+    uint32_t h[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t w8 = wd[i] >> 8;
+      h[4 * i + 0] = (wd[i] & mlo) | mag;
+      h[4 * i + 1] = (wd[i] & mhi) | mag;
+      h[4 * i + 2] = (w8 & mlo) | mag;
+      h[4 * i + 3] = (w8 & mhi) | mag;
+    }
+    const f16x2 sm2 = as_h2(sm[rd]);
+    const float s = (float)sm2.x, mn = (float)sm2.y;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      const u32x4 *x4 = (const u32x4 *)(sX + (size_t)m * p.K + u * UK);
+      float dlo = 0.0f, dhi = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const u32x4 xv = x4[i];
+        dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), dlo, false);
+        dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), dhi, false);
+        dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), dlo, false);
+        dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), dhi, false);
+      }
+      const f32x2 g = sG[m * (nb / 4u) + u];
+      const float t = fmaf(-1024.0f, g.x, dlo) + 0.0625f * fmaf(-1024.0f, g.y, dhi);   // sum x q, exact for e_k
+      acc[m] = fmaf(s, t, fmaf(mn, g.x + g.y, acc[m]));
+    }
+  }
+  // the row's four lanes (l, l + 16, l + 32, l + 48) in a fixed order, then the waves in wave order
+  float *sR = (float *)sn_smem;                                // [wave][MT][16] after a barrier (X' is dead)
+#pragma unroll
+  for (int m = 0; m < MT; m++) {
+    acc[m] += __shfl_xor(acc[m], 16);
+    acc[m] += __shfl_xor(acc[m], 32);
+  }
+  __syncthreads();
+  if (us == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; m++) sR[(wave * MT + m) * SN_ROWS + ri] = acc[m];
+  }
+  __syncthreads();
+  const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+  auto tot = [&](uint32_t m, uint32_t i) {
+    float v = sR[m * SN_ROWS + i];
+#pragma unroll
+    for (int w = 1; w < SN_NT / 64; w++) v += sR[(w * MT + m) * SN_ROWS + i];
+    return v;
+  };
+  if (glu) {                                                                      // gemm.js:204-210
+    const uint32_t Nout = p.N >> 1;
+    const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
+    if ((uint32_t)tid < rows * 8u) {
+      const uint32_t m = tid / 8, c = tid % 8, o = (nB >> 1) + c;
+      if (o < Nout) {
+        float gt = tot(m, c), u = tot(m, 8 + c);
+        if (bias) { gt += p.BV[p.bvOff + o]; u += p.BV[p.bvOff + p.bvUp + o]; }
+        ((uint16_t *)p.Y)[(size_t)m * p.ldy + p.ny0 + o] = h_bits(glu_act(gt, gelu) * u);
+      }
+    }
+    return;
+  }
+  if ((uint32_t)tid < rows * SN_ROWS) {
+    const uint32_t m = tid / SN_ROWS, c = tid % SN_ROWS, col = nB + c;
+    if (col >= p.N) return;
+    const float v = tot(m, c);
+    const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
+    if (p.epi == E_F16) {                                                         // gemm.js:194-196
+      ((uint16_t *)p.Y)[yi] = h_bits(v);
+    } else if (p.epi == E_F32) {
+      ((float *)p.Y)[yi] = v;
+    } else if (p.epi == E_BIAS) {                                                 // gemm.js:211-215
+      float rr = v + p.EV[p.evOff + col];
+      if (p.flags & F_RES) rr += h_val(((const uint16_t *)p.Y)[yi]);
+      ((uint16_t *)p.Y)[yi] = h_bits(rr);
+    } else {                                                                      // resadd, gemm.js:197-203
+      const float g = (p.flags & F_GATE) ? p.EV[p.evOff + col] : 1.0f;
+      const float b = (p.flags & F_BIAS) ? p.BV[p.bvOff + col] : 0.0f;
+      float *y = (float *)p.Y + yi;
+      *y = ((p.flags & F_STORE) ? 0.0f : *y) + g * (v + b);
+    }
+  }
+}
+
+// rounds of 32 units (1024 k) a short-call item takes, the longest K it serves and its LDS bytes
+constexpr int SN_RND_MAX = 16;
+unsigned gemv_sn_kmax() { return SN_RND_MAX * 32u * 32u; }
+static uint32_t sn_lds(uint32_t M, uint32_t K) { return M * K * 2u + M * (K / 32u) * 8u; }
+
+template <int XM, int MT>
+static hipError_t launch_sn_mt(const Params &p, hipStream_t s) {
+  const uint32_t rounds = (p.K / 32u + 31u) / 32u;
+  const uint32_t lds = sn_lds(MT, p.K);
+  const dim3 grid((p.N + SN_ROWS - 1) / SN_ROWS);
+#define SN_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn<XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
+  switch (rounds <= 4 ? 4 : rounds <= 8 ? 8 : rounds <= 12 ? 12 : 16) {
+    SN_CASE(4) SN_CASE(8) SN_CASE(12) SN_CASE(16)
+  default: return hipErrorInvalidValue;
+  }
+#undef SN_CASE
+  return hipGetLastError();
+}
+template <int XM>
+static hipError_t launch_sn_x(const Params &p, hipStream_t s) {
+  if (p.M == 1) return launch_sn_mt<XM, 1>(p, s);
+  if (p.M == 2) return launch_sn_mt<XM, 2>(p, s);
+  return launch_sn_mt<XM, 4>(p, s);
+}
+hipError_t launch_gemv_sn(const Params &p, int xm, hipStream_t s) {
+  if (p.M == 0 || p.M > 4 || p.K % 32 || p.K > gemv_sn_kmax() || p.wk0 % 32 || p.epi == E_HEADS ||
+      p.epi == E_ONORMGATE || sn_lds(p.M <= 2 ? p.M : 4, p.K) > 64u * 1024u)
+    return hipErrorInvalidValue;
+  switch (xm) {
+  case X_F16: return launch_sn_x<X_F16>(p, s);
+  case X_LNMOD: return launch_sn_x<X_LNMOD>(p, s);
+  case X_RMS: return launch_sn_x<X_RMS>(p, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // Decode on the matrix cores (q4 with 3..16 rows when k_gemv_mq4 is switched off, M <= 16 for q8 / f16). With several rows of X the per-row dot products of the stream above
 // multiply its VALU work; here the same items, waves and ring feed v_mfma_f32_16x16x32_f16 instead. Per 32-k step
 // (q4, f16; 64-k for q8) a wave runs one MFMA per block of 16 of its 64 weight rows: A = X' (16 rows, zero past M),

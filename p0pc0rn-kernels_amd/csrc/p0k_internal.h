@@ -6,7 +6,7 @@
 
 namespace p0k {
 struct Params;
-enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2, K_MFMA_DMA = 3 };
+enum { K_MFMA = 0, K_GEMV = 1, K_GEMV_MF = 2, K_MFMA_DMA = 3, K_GEMV_SN = 4 };
 // kernel choice of one call: GEMV items are (128-column tile) x (K slice of KS), S slices per tile
 struct Plan { int kernel, we, xm; unsigned bm, bn, S, KS; bool mx, narrow; };
 // What the kernel choice depends on besides the call: the device's CU count and the P0K_* tuning switches of the
@@ -19,6 +19,7 @@ struct Tuning {
   unsigned gemv_slices = 0;    // P0K_GEMV_SLICES=n: decode K slices (0: not set)
   unsigned gemv_mx = 4;        // P0K_GEMV_MX=n: q4 decode with 2..n rows on the stream kernel's matrix-core form
   bool gemv_narrow = true;     // P0K_GEMV_NARROW=0: no 64-column decode items (a K split fills the GPU instead)
+  int gemv_sn = -1;            // P0K_GEMV_SN=0|1: short-call decode items of 16 rows never / wherever they apply
   bool mfma_reg = false;       // P0K_MFMA_KERNEL=reg: the register-staged MFMA kernel
   unsigned tile_m = 0, tile_n = 0;   // P0K_MFMA_TILE=MxN
   bool dma_tail = true;        // P0K_DMA_TAIL=0: one launch for a mostly empty last round

@@ -35,6 +35,10 @@ unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx);   // longest K slice
 unsigned gemv_unit_k(int we, bool mf);                      // k of one decode weight unit
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s,
                        bool mf, bool mq4, bool mx, bool narrow);
+// short decode calls: q4, 1..4 rows, element-wise epilogues, K % 32 == 0 and K <= gemv_sn_kmax(); items of 16 weight
+// rows with no K split (ceil(N / 16) workgroups)
+unsigned gemv_sn_kmax();
+hipError_t launch_gemv_sn(const Params &p, int xm, hipStream_t s);
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);

@@ -512,7 +512,9 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
   p.GT = (const uint16_t *)a->gt_buf;
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
   hipError_t e;
-  if (plan.kernel == p0k::K_GEMV || plan.kernel == p0k::K_GEMV_MF) {
+  if (plan.kernel == p0k::K_GEMV_SN) {
+    e = p0k::launch_gemv_sn(p, plan.xm, c->stream);
+  } else if (plan.kernel == p0k::K_GEMV || plan.kernel == p0k::K_GEMV_MF) {
     const uint32_t tiles = (a->N + 127) / 128;
     float *part = nullptr;
     if (plan.S > 1) {

@@ -349,7 +349,7 @@ static napi_value selectTile(napi_env env, napi_callback_info info) {
   napi_create_object(env, &o);
   napi_set_named_property(env, o, "BM", mk_num(env, t.bm));
   napi_set_named_property(env, o, "BN", mk_num(env, t.bn));
-  napi_create_string_utf8(env, t.kernel == 1 ? "gemv" : t.kernel == 2 ? "gemv_mfma" : t.kernel == 3 ? "mfma_dma" : "mfma", NAPI_AUTO_LENGTH, &s);
+  napi_create_string_utf8(env, t.kernel == 1 ? "gemv" : t.kernel == 2 ? "gemv_mfma" : t.kernel == 3 ? "mfma_dma" : t.kernel == 4 ? "gemv_short" : "mfma", NAPI_AUTO_LENGTH, &s);
   napi_set_named_property(env, o, "kernel", s);
   return o;
 }

@@ -285,7 +285,7 @@ class Buffer:
         self.ptr, self.size, self.dev = ptr, size, dev
 
 
-TUNING_SWITCHES = ("P0K_MFMA_TILE", "P0K_MFMA_KERNEL", "P0K_DMA_TAIL", "P0K_GEMV_MF", "P0K_GEMV_MQ4", "P0K_GEMV_MX", "P0K_GEMV_NARROW", "P0K_GEMV_SLICES",
+TUNING_SWITCHES = ("P0K_MFMA_TILE", "P0K_MFMA_KERNEL", "P0K_DMA_TAIL", "P0K_GEMV_MF", "P0K_GEMV_MQ4", "P0K_GEMV_MX", "P0K_GEMV_NARROW", "P0K_GEMV_SN", "P0K_GEMV_SLICES",
                    "P0K_ATTN_BQ")
 
 
@@ -522,4 +522,4 @@ def select_tile(a):
 
 
 def _tile_dict(t):
-    return {"BM": t.bm, "BN": t.bn, "kernel": {1: "gemv", 2: "gemv_mfma", 3: "mfma_dma"}.get(t.kernel, "mfma")}
+    return {"BM": t.bm, "BN": t.bn, "kernel": {1: "gemv", 2: "gemv_mfma", 3: "mfma_dma", 4: "gemv_short"}.get(t.kernel, "mfma")}

@@ -140,10 +140,11 @@ def test_conv3_frame_window_checked():
 
 
 def test_kernel_choice():
-    assert p0k.select_tile(host_args(make_case(M=1, enc="q4g32a.t64")))["kernel"] == "gemv"
+    assert p0k.select_tile(host_args(make_case(M=1, enc="q4g32a.t64")))["kernel"] == "gemv_short"   # short call
     assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv_mfma"              # f16 / q8 rows: matrix cores
     assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
-    assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, 2..4 rows: stream
+    assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv_short"
+    assert p0k.select_tile(host_args(make_case(M=3, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, 3..4 rows: stream
     assert p0k.select_tile(host_args(make_case(M=4, enc="q4g32a.t64")))["kernel"] == "gemv"
     assert p0k.select_tile(host_args(make_case(M=5, enc="q4g32a.t64")))["kernel"] == "gemv_mfma"
     assert p0k.select_tile(host_args(make_case(M=16)))["kernel"] == "gemv_mfma"
@@ -219,6 +220,7 @@ def test_decode_row_routing_switch(monkeypatch):
     """P0K_GEMV_MX=n sends q4 decode calls with 2..n rows to the stream kernel's matrix-core form (kernel "gemv");
     the default is 4, beyond it the q4 matrix-core decode (k_gemv_mq4, "gemv_mfma") takes the call."""
     q4 = lambda M: p0k.select_tile(host_args(make_case(M=M, enc="q4g32a.t64", N=256, K=512)))["kernel"]   # noqa: E731
+    monkeypatch.setenv("P0K_GEMV_SN", "0")                        # (these short calls would take the 16-row items)
     assert [q4(M) for M in (1, 2, 3, 4, 5, 16)] == ["gemv"] * 4 + ["gemv_mfma"] * 2
     monkeypatch.setenv("P0K_GEMV_MX", "0")
     assert [q4(M) for M in (1, 2, 3, 4)] == ["gemv", "gemv", "gemv_mfma", "gemv_mfma"]
@@ -226,6 +228,24 @@ def test_decode_row_routing_switch(monkeypatch):
     assert [q4(M) for M in (5, 8, 16)] == ["gemv"] * 3
     # q8 / f16 weights never take it
     assert p0k.select_tile(host_args(make_case(M=4, enc="q8g64s.t64", N=256, K=512)))["kernel"] == "gemv_mfma"
+
+
+def test_short_decode_routing(monkeypatch):
+    """q4 decode with one or two rows whose 16-row items number at most about one per CU (1.5 per CU at one row), K up to
+    8192 and an element-wise epilogue takes the short-call kernel; P0K_GEMV_SN=0 / 1 switch it off / on wherever it
+    can run (up to 4 rows, K up to 16384)."""
+    q4 = lambda M, N, K, **kw: p0k.select_tile(host_args(make_case(M=M, enc="q4g32a.t64", N=N, K=K, **kw)))["kernel"]   # noqa: E731
+    assert q4(1, 4096, 4096) == "gemv_short" and q4(2, 4096, 4096) == "gemv_short"
+    assert q4(1, 6144, 4096) == "gemv_short" and q4(2, 6144, 4096) == "gemv"
+    assert q4(1, 14336, 4096) == "gemv" and q4(4, 4096, 4096) == "gemv" and q4(1, 4096, 16384) == "gemv"
+    assert q4(1, 2048, 1024, epi="swiglu") == "gemv_short"
+    assert q4(1, 384, 256, epi="heads", Hq=1, Hkv=1) != "gemv_short"
+    assert p0k.select_tile(host_args(make_case(M=1, enc="q8g64s.t64", N=256, K=512)))["kernel"] == "gemv_mfma"
+    monkeypatch.setenv("P0K_GEMV_SN", "0")
+    assert q4(1, 4096, 4096) == "gemv"
+    monkeypatch.setenv("P0K_GEMV_SN", "1")
+    assert q4(1, 14336, 4096) == "gemv_short" and q4(1, 4096, 16384) == "gemv_short" and q4(4, 4096, 4096) == "gemv_short" and q4(3, 520, 96) == "gemv_short"
+    assert q4(1, 4096, 16416) != "gemv_short" and q4(4, 4096, 8192) != "gemv_short"   # past the longest K an item stages
 
 
 def test_null_context_calls_are_refused():

@@ -103,10 +103,18 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    assert kern == ("gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else "mfma_dma")
+    short = M <= 2 and enc.startswith("q4") and epi not in ("heads", "onormgate")
+    assert kern == ("gemv_short" if short else "gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else
+                    "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
+    if short:
+        # the one-row / 2-row stream kernel on the same call (P0K_GEMV_SN=0)
+        monkeypatch.setenv("P0K_GEMV_SN", "0")
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
+        got = c.run_device(dev)
+        assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M} stream")
     if kern == "mfma_dma":
         # the register-staged MFMA kernel on the same call
         monkeypatch.setenv("P0K_MFMA_KERNEL", "reg")
@@ -151,6 +159,7 @@ def test_matrix_core_stream_long_k(dev, M, K, slices, monkeypatch):
     these 4 column tiles), against the oracle's CPU weight model."""
     if slices:
         monkeypatch.setenv("P0K_GEMV_SLICES", str(slices))
+    monkeypatch.setenv("P0K_GEMV_SN", "0")                        # (M = 2 would take the short-call items)
     banner(f"matrix-core stream M={M} K={K} slices={slices}")
     c = make_case(enc="q4g32a.t64", epi="swiglu", M=M, N=512, K=K, seed=41)
     assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
@@ -214,6 +223,7 @@ def test_narrow_decode_items(dev, epi, M, N, K, narrow, monkeypatch):
     items in K slices meeting through the workspace; both against the oracle's CPU weight model, ragged last items
     included."""
     monkeypatch.setenv("P0K_GEMV_NARROW", "1" if narrow else "0")
+    monkeypatch.setenv("P0K_GEMV_SN", "0")                        # (N 4096 at one row would take the short-call items)
     banner(f"narrow={narrow} {epi} M={M} N={N} K={K}")
     c = make_case(enc="q4g32a.t64", epi=epi, M=M, N=N, K=K, seed=91)
     t = dev.select_tile(c.args(lambda n: c.bufs[n]))
@@ -265,15 +275,17 @@ def _adversarial_q8(rows, K, seed):
 
 
 @pytest.mark.parametrize("enc", ["q4g32a.t64", "q8g64s.t64"])
-@pytest.mark.parametrize("path", ["gemv", "gemv_mx2", "gemv_mx8", "gemv_mx16", "gemv_mfma", "gemv_mfma_staged", "mfma"])
+@pytest.mark.parametrize("path", ["gemv", "gemv_short", "gemv_short4", "gemv_mx2", "gemv_mx8", "gemv_mx16", "gemv_mfma",
+                                  "gemv_mfma_staged", "mfma"])
 def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     """X = unit rows e_k: each output is ONE product 1.0 * W'[n, k], so the fp16 output is the decoded weight itself,
     which must equal the oracle's f16(f32(q*s + mn)) / f16(q*s) bit for bit — on random codes and scale words chosen
     to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream;
     P0K_GEMV_MX=16 the stream kernel's 4x4x4 matrix-core form for q4 with 2..16 rows; P0K_GEMV_MQ4=0 the q4
     matrix-core decode with X' staged in LDS.)"""
-    if path.startswith("gemv_mx") and not enc.startswith("q4"):
-        pytest.skip("the stream kernel's matrix-core form is q4 only")
+    if (path.startswith("gemv_mx") or path.startswith("gemv_short")) and not enc.startswith("q4"):
+        pytest.skip("the stream kernel's matrix-core form and the short-call kernel are q4 only")
+    monkeypatch.setenv("P0K_GEMV_SN", "1" if path.startswith("gemv_short") else "0")
     if path == "gemv":
         monkeypatch.setenv("P0K_GEMV_MF", "0")
     if path.startswith("gemv_mx"):
@@ -285,7 +297,7 @@ def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     want = oracle.dequant(enc, wb, rows, K)                                  # [rows][K] fp16 bits
     dw = dev.upload(wb)
     try:
-        M = {"gemv": 1, "gemv_mx2": 2, "gemv_mx8": 8, "gemv_mx16": 16, "gemv_mfma": 16, "gemv_mfma_staged": 16, "mfma": K}[path]
+        M = {"gemv": 1, "gemv_short": 1, "gemv_short4": 4, "gemv_mx2": 2, "gemv_mx8": 8, "gemv_mx16": 16, "gemv_mfma": 16, "gemv_mfma_staged": 16, "mfma": K}[path]
         got = np.zeros((K, rows), np.uint16)
         for k0 in range(0, K, M):
             X = np.zeros((M, K), np.float32)
@@ -655,3 +667,35 @@ def test_workspace_growth_stays_bounded(dev):
     finally:
         for b in d.values():
             dev.free(b)
+
+
+SHORT_CASES = [
+    dict(M=1, N=4096, K=4096, epi="f16"),
+    dict(M=2, N=136, K=96, epi="f32"),
+    dict(M=3, N=24, K=1056, epi="bias", bias=True, res=True),
+    dict(M=1, N=520, K=16384, epi="resadd", gate=True, bias=True),
+    dict(M=4, N=4096, K=4096, epi="resadd", gate=True, bias=True),
+    dict(M=1, N=512, K=2048, epi="swiglu", bias=True),
+    dict(M=2, N=272, K=3072, epi="swiglu", act="gelu"),
+    dict(M=1, N=256, K=512, epi="resadd", store=True, xmode="rms"),
+    dict(M=2, N=128, K=1024, epi="f16", xmode="lnmod"),
+    dict(M=4, N=64, K=4096, epi="swiglu", xmode="rms", bias=True),
+    dict(M=1, N=200, K=256, epi="f16", ld_pad=8, k0=64, wk0=32, n0=8),
+    dict(M=2, N=96, K=160, epi="swiglu", wr0=64, ld_pad=16),
+]
+
+
+@pytest.mark.parametrize("kw", SHORT_CASES, ids=lambda k: f"M{k['M']}-N{k['N']}-K{k['K']}-{k.get('xmode', 'f16')}-{k['epi']}")
+def test_short_decode_matches_oracle(dev, kw, monkeypatch):
+    """The short-call decode (16-row items, every load in flight at once, P0K_GEMV_SN=1 forces it): 1..4 rows, K from
+    one unit to its longest (16384), K not a multiple of the 1024-k round, N not a multiple of the item, every
+    element-wise epilogue (bias / residual / gate / store / SwiGLU / GeGLU), the rms / lnmod prologues, X pitch and
+    column offsets, weight column and row offsets, output column offset; against the oracle's CPU weight model (the
+    algebraic form of the decode kernels)."""
+    monkeypatch.setenv("P0K_GEMV_SN", "1")
+    kw = dict(kw)
+    c = make_case(enc="q4g32a.t64", seed=61 + kw["K"] % 97, wscale=0.02, **kw)
+    banner(f"short decode {kw}")
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short {kw}")
