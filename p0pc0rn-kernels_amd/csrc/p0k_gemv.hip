@@ -491,7 +491,11 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ri = lane & 15, us = lane >> 4;
   const bool glu = p.epi == E_SWIGLU;
-  const uint32_t nB = blockIdx.x * (uint32_t)SN_ROWS;
+  // workgroups go to the 8 XCDs in turn: give each XCD a contiguous run of items, so the four items of a 64-row record
+  // block (and their shared 128-byte lines of scale words) meet in one L2 instead of four
+  const uint32_t nit = gridDim.x;
+  const uint32_t item = (nit & 7u) ? blockIdx.x : (blockIdx.x & 7u) * (nit >> 3) + (blockIdx.x >> 3);
+  const uint32_t nB = item * (uint32_t)SN_ROWS;
   const uint32_t wsc = glu ? (ri < 8 ? 2u * ri : 2u * (ri - 8) + 1u) : (uint32_t)ri;
   const uint32_t r = wrow(p, nB + wsc);
   const uint32_t nun = p.K / UK;                               // units (32 k) of the call
