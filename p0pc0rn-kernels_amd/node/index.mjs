@@ -228,9 +228,10 @@ function gemm(gpu, a) {
   return call(addon().gemm, gpu.ctx, d);
 }
 
-/** the kernel and tile libp0k runs for these arguments ({kernel: 'gemv'|'mfma', BM, BN}); checks them like gemm does */
+/** the kernel and tile libp0k runs for these arguments on this gpu's device ({kernel: 'gemv'|'gemv_short'|'gemv_mfma'|
+ *  'mfma_dma'|'mfma', BM, BN}); checks them like gemm does */
 function gemmPlan(gpu, a) {
-  return call(addon().selectTile, gemmDesc(gpu, a));
+  return call(addon().selectTile, gemmDesc(gpu, a), gpu ? gpu.ctx : undefined);
 }
 
 /** per-row statistics of an f16 / f32 matrix: ST[(st.off+r)*2] = mean (mode 'ln') or 0 (mode 'rms'), ST[..+1] = rstd */

@@ -337,13 +337,14 @@ static napi_value gemmCheck(napi_env env, napi_callback_info info) {   /* (desc)
   return undef(env);
 }
 
-static napi_value selectTile(napi_env env, napi_callback_info info) {
-  napi_value argv[1];
-  if (!get_args(env, info, 1, argv)) return NULL;
+static napi_value selectTile(napi_env env, napi_callback_info info) {   /* (desc[, ctx]): with a context, its plan */
+  napi_value argv[2];
+  if (!get_args(env, info, 2, argv)) return NULL;
   p0k_gemm_args a;
   if (!parse_gemm(env, argv[0], &a)) return NULL;
   p0k_tile t;
-  int r = p0k_select_tile(&a, &t);
+  p0k_ctx *ctx = get_ctx(env, argv[1]);
+  int r = ctx ? p0k_gemm_plan(ctx, &a, &t) : p0k_select_tile(&a, &t);
   if (r) return throw_p0k(env, r);
   napi_value o, s;
   napi_create_object(env, &o);
