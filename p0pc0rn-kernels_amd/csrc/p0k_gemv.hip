@@ -640,7 +640,11 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
 // rounds of 32 units (1024 k) a short-call item takes, the longest K it serves and its LDS bytes
 constexpr int SN_RND_MAX = 16;
 unsigned gemv_sn_kmax() { return SN_RND_MAX * 32u * 32u; }
-static uint32_t sn_lds(uint32_t M, uint32_t K) { return M * K * 2u + M * (K / 32u) * 8u; }
+// X' and its per-unit sums; after the stream the same buffer holds the waves' partials (8 waves x M x 16 floats)
+static uint32_t sn_lds(uint32_t M, uint32_t K) {
+  const uint32_t x = M * K * 2u + M * (K / 32u) * 8u, r = (uint32_t)(SN_NT / 64) * M * SN_ROWS * 4u;
+  return x > r ? x : r;
+}
 
 template <int XM, int MT>
 static hipError_t launch_sn_mt(const Params &p, hipStream_t s) {

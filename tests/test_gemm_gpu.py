@@ -672,6 +672,7 @@ def test_workspace_growth_stays_bounded(dev):
 SHORT_CASES = [
     dict(M=1, N=4096, K=4096, epi="f16"),
     dict(M=2, N=136, K=96, epi="f32"),
+    dict(M=4, N=40, K=32, epi="f16"),          # one unit: the partials need more LDS than X' does
     dict(M=3, N=24, K=1056, epi="bias", bias=True, res=True),
     dict(M=1, N=520, K=16384, epi="resadd", gate=True, bias=True),
     dict(M=4, N=4096, K=4096, epi="resadd", gate=True, bias=True),
