@@ -182,7 +182,8 @@ int p0k_device_info_get(p0k_ctx *ctx, p0k_device_info *out);
 int p0k_ctx_reload_env(p0k_ctx *ctx);
 int p0k_ctx_cus(p0k_ctx *ctx);
 /* The context's HIP stream (a hipStream_t), for callers that enqueue their own work in order with the context's (no
- * counterpart in the reference, whose queue is gpu.device.queue, src/core/gpu.js:15-20). */
+ * counterpart in the reference, whose queue is gpu.device.queue, src/core/gpu.js:15-20). A caller may capture it into
+ * a graph of its own: gemm calls enqueued under any capture keep the workspaces they use alive until the context goes. */
 void *p0k_ctx_stream(p0k_ctx *ctx);
 /* Device bytes held by the context's gemm workspaces (split-decode partials, the rms / lnmod X'), and how many
  * replaced workspaces it keeps because a graph captured after they were allocated may still address them. */

@@ -505,6 +505,16 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
       if (int rr = check_operand(c, o.b, o.s, o.n)) return rr;
   }
   if (a->M == 0 || a->N == 0) return P0K_OK;
+  {
+    // a call enqueued while the stream is being captured (p0k_graph_begin, or a caller's own capture of
+    // p0k_ctx_stream) may put the current workspaces into a graph: from here on they are kept when replaced
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIPCHK(hipStreamIsCapturing(c->stream, &cs), "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone) {
+      std::lock_guard<std::mutex> lk(c->mu);
+      c->graph_epoch++;
+    }
+  }
   p.W = (const uint8_t *)a->w_buf + a->w_off;
   p.X = (const uint8_t *)a->x_buf + a->x_off;
   p.Y = (uint8_t *)a->y_buf + a->y_off;

@@ -700,3 +700,44 @@ def test_short_decode_matches_oracle(dev, kw, monkeypatch):
     assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short {kw}")
+
+
+def test_caller_captured_stream_keeps_its_workspace(dev):
+    """A caller that captures the context's stream itself (p0k_ctx_stream + the HIP graph API) around an rms call:
+    a later call that grows the X' workspace must keep the one the caller's graph uses, and the graph replays
+    correctly."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    stream = p0k.lib().p0k_ctx_stream(dev.ctx)
+    assert stream
+    K = 512
+    c = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=64, N=128, K=K, seed=99)
+    d = {k: dev.upload(v) for k, v in c.bufs.items()}
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        a = c.args(lambda n: d[n])
+        dev.gemm(a)                                    # sizes the workspace outside the capture
+        dev.done()
+        assert hip.hipStreamBeginCapture(C.c_void_p(stream), 1) == 0          # thread-local capture mode
+        try:
+            dev.gemm(a)
+        finally:
+            assert hip.hipStreamEndCapture(C.c_void_p(stream), C.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)) == 0
+        before = dev.workspace_stats()
+        Mbig = (before["live_bytes"] // (2 * K) + 64 + 63) // 64 * 64
+        big = make_case(enc="q8g64s.t64", xmode="rms", epi="f16", M=Mbig, N=128, K=K, seed=100)
+        print(f"[p0k-test] growth past a caller's capture: M={Mbig}", flush=True)
+        big.run_device(dev)
+        assert dev.workspace_stats()["retired_buffers"] == before["retired_buffers"] + 1
+        dev.upload(np.zeros_like(c.bufs["y"]), d["y"])
+        assert hip.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
+        dev.done()
+        assert_close(dev.read(d["y"], np.uint16, c.bufs["y"].size), c.run_oracle(), what="caller's graph replay")
+    finally:
+        if exe:
+            hip.hipGraphExecDestroy(exe)
+        if graph:
+            hip.hipGraphDestroy(graph)
+        for b in d.values():
+            dev.free(b)
