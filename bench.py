@@ -571,7 +571,8 @@ def library_gemm():
     import torch
     lib = []
     for (m, n, k, what) in ((2048, 4096, 4096, "configs[2] shape"), (4096, 9216, 3072, "DiT QKV shape"),
-                            (4096, 24576, 3072, "DiT up shape (weight rows)"), (4096, 4096, 4096, "4096^3")):
+                            (4096, 24576, 3072, "DiT up shape (weight rows)"), (4096, 4096, 4096, "4096^3"),
+                            (191360, 128, 3456, "conv3 shape, X materialised (1.32 GB)")):
         g = torch.Generator(device="cuda").manual_seed(7)
         a = torch.randn(m, k, device="cuda", dtype=torch.float16, generator=g)
         b = torch.randn(n, k, device="cuda", dtype=torch.float16, generator=g) * 0.02
