@@ -299,6 +299,7 @@ BUILDERS = {
     "decode1_plain": lambda d: decode_q4(d, 1, glu=False),
     "decode1_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096),
     "decode1_q8": lambda d: decode_q4(d, 1, glu=False, enc="q8g64s.t64"),
+    "decode1_q8_proj": lambda d: decode_q4(d, 1, glu=False, n_out=4096, enc="q8g64s.t64"),
     "hbm_ceiling_proj": lambda d: hbm_ceiling(d, 256, 256, nbytes=4096 // 64 * (4096 // 32) * 1280,
                                               name="hbm_read_ceiling_10MB"),
     "prefill": prefill_q8, "prefill_f16res": prefill_q8_f16res, "prefill_rowstats": prefill_rowstats,

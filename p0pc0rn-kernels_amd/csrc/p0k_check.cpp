@@ -75,14 +75,22 @@ Tuning tuning_from_env(unsigned cus) {
   return t;
 }
 
-// Where the short-call decode items are taken: at most about one 16-row item per CU (one and a half at one row), one
-// or two rows, K up to 8192. Measured per call against the planner's other choice (ring kernels, 64-column items or a
-// K split), q4, K 4096 unless stated: plain N 2048 M 1 3.88 vs 6.07 us, M 2 5.35 vs 6.79; N 4096 M 1 4.45 vs 6.17,
+// Where the short-call decode items are taken. q4: at most about one 16-row item per CU (one and a half at one row),
+// one or two rows, K up to 8192. Measured per call against the planner's other choice (ring kernels, 64-column items or
+// a K split), q4, K 4096 unless stated: plain N 2048 M 1 3.88 vs 6.07 us, M 2 5.35 vs 6.79; N 4096 M 1 4.45 vs 6.17,
 // M 2 6.06 vs 6.89, M 4 7.92 vs 7.35; N 6144 M 1 6.02 vs 6.43, M 2 7.77 vs 7.08; N 14336 M 1 9.71 vs 7.98; N 4096
 // K 8192 M 1 7.81 vs 9.98; K 14336 12.0 vs 11.9; SwiGLU out 4096 (8192 weight rows) M 1 7.91 vs 7.57. (A plain
 // one-launch read of the same 10.5 MB as N 4096 K 4096 takes 4.3-4.5 us: the short calls are latency, not bytes.)
-static bool sn_rule(uint32_t N, uint32_t K, uint32_t M, unsigned cus) {
+// q8 (against the matrix-core decode): every q8 call with up to 3.5 items per CU at one row, 2 at two rows and 1 at
+// 3..4 rows, K up to 8192 (all that fits): plain N 4096 K 4096 M 1 / 2 / 4 5.21 / 6.67 / 8.57 vs 9.58 / 9.71 / 9.95 us;
+// N 2048 4.44 / 5.91 / 7.68 vs 9.34 / 9.50 / 9.70; K 2048 4.12 / 4.76 / 5.88 vs 6.99 / 7.10 / 7.28; N 8192 M 1 / 2
+// 7.48 / 9.68 vs 10.16 / 10.25 (M 4 13.17 vs 10.49); N 14336 M 1 11.93 vs 12.69 (M 2 15.13 vs 12.59); N 4096 K 8192
+// M 1 / 2 9.47 / 11.31 vs 13.56 / 13.71; SwiGLU out 4096 M 1 / 2 7.64 / 9.66 vs 11.69 / 11.74, out 7168 M 1 12.15 vs
+// 13.93; N 6144 M 4 11.95 vs 10.29, N 10240 M 2 11.64 vs 10.71 (not taken).
+static bool sn_rule(int we, uint32_t N, uint32_t K, uint32_t M, unsigned cus) {
   const uint64_t items = (N + 15u) / 16u;
+  if (we == P0K_ENC_Q8G64S_T64)
+    return K <= 8192u && (M == 1 ? items * 2u <= (uint64_t)cus * 7u : M == 2 ? items <= (uint64_t)cus * 2u : items <= cus);
   return M <= 2 && K <= 8192u && items * 2u <= (uint64_t)cus * (M == 1 ? 3u : 2u);
 }
 
@@ -312,11 +320,13 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
         if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
-      // short calls (q4, up to 4 rows, element-wise epilogues): 16-row items, no K split, every load of an item in
-      // flight at once (SHORT_RULE below)
-      const bool sn_ok = we == P0K_ENC_Q4G32A_T64 && M <= 4 && epi != P0K_EPI_HEADS && epi != P0K_EPI_ONORMGATE &&
-                         K <= gemv_sn_kmax() && a->wk0 % 32 == 0 && (uint64_t)(M <= 2 ? M : 4) * K * 2 + (uint64_t)(M <= 2 ? M : 4) * (K / 32) * 8 <= 64u * 1024u;
-      if (sn_ok && (tune.gemv_sn == 1 || (tune.gemv_sn < 0 && sn_rule(N, K, M, tune.cus)))) {
+      // short calls (q4 or q8, up to 4 rows, element-wise epilogues): 16-row items, no K split, every load of an item
+      // in flight at once (sn_rule above)
+      const uint32_t snuk = we == P0K_ENC_Q8G64S_T64 ? 64u : 32u;
+      const bool sn_ok = (we == P0K_ENC_Q4G32A_T64 || we == P0K_ENC_Q8G64S_T64) && M <= 4 && epi != P0K_EPI_HEADS &&
+                         epi != P0K_EPI_ONORMGATE && K % snuk == 0 && K <= gemv_sn_kmax(we) && a->wk0 % snuk == 0 &&
+                         gemv_sn_lds(we, M <= 2 ? M : 4, K) <= 64u * 1024u;
+      if (sn_ok && (tune.gemv_sn == 1 || (tune.gemv_sn < 0 && sn_rule(we, N, K, M, tune.cus)))) {
         kernel = K_GEMV_SN;
         S = 1;
         KS = K;

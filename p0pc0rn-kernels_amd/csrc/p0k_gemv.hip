@@ -475,21 +475,31 @@ __global__ __launch_bounds__(GV_NT) void k_gemv(Params p, float *part, uint32_t 
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Short decode calls (q4, 1..4 rows, element-wise epilogues): items of 16 weight rows, so that even N = 4096 gives one
-// item per CU with no K split. A call of this size is mostly latency (launch, the first bytes' trip from HBM, the
+// Short decode calls (q4 or q8, 1..4 rows, element-wise epilogues): items of 16 weight rows, so that even N = 4096 gives
+// one item per CU with no K split. A call of this size is mostly latency (launch, the first bytes' trip from HBM, the
 // finish), and a ring per lane keeps only a few units in flight per CU; here every lane issues all of its weight loads
 // at once (the whole item, 16 rows x K, is in flight on the CU right after the launch), X' is staged in LDS with its
-// per-unit sums while those loads travel, and each lane reduces its units with the same algebraic form as k_gemv. Lane
-// l of a wave owns row l % 16 of the item and unit l / 16 of every round of 4 units; the 8 waves take rounds of 32
-// consecutive units (wave w the units 4 w .. 4 w + 3 of each). The four lanes of a row meet by DPP, the waves in LDS
-// (wave order), and one thread per output element applies the epilogue. With the SwiGLU interleave, rows 0..7 of an
-// item are 8 consecutive gate rows and rows 8..15 the matching up rows.
+// per-unit sums while those loads travel, and each lane reduces its units with the same algebraic form as k_gemv. The
+// 8 waves take rounds of 32 consecutive units (wave w the units 4 w .. 4 w + 3 of each). q4 (32-k units of 16 bytes
+// per row): lane l of a wave owns row l % 16 and unit l / 16 of every round, so one load instruction reads four
+// 256-byte runs of 16 whole code rows. q8 (64-k units of 64 bytes per row): lane l owns row (l / 4) % 16 and the
+// 16-byte chunk l % 4 of all four units of the round, so one load instruction reads one unit's 1 KB of code rows
+// whole. The four lanes of a row meet by DPP, the waves in LDS (wave order), and one thread per output element applies
+// the epilogue. With the SwiGLU interleave, rows 0..7 of an item are 8 consecutive gate rows and rows 8..15 the
+// matching up rows.
 constexpr int SN_NT = 512, SN_ROWS = 16;
-template <int XM, int MT, int RND>
+template <int WE>
+struct SnUnit;
+template <>
+struct SnUnit<W_Q4> { static constexpr int UK = 32, NC = 1; };
+template <>
+struct SnUnit<W_Q8> { static constexpr int UK = 64, NC = 4; };
+
+template <int WE, int XM, int MT, int RND>
 __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
-  constexpr int UK = 32;
+  constexpr int UK = SnUnit<WE>::UK, NC = SnUnit<WE>::NC, CPU_ = UK / 8;   // k per unit, code loads, 8-k chunks
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ri = lane & 15, us = lane >> 4;
+  const int ri = WE == W_Q8 ? (lane >> 2) & 15 : lane & 15, us = WE == W_Q8 ? lane & 3 : lane >> 4;
   const bool glu = p.epi == E_SWIGLU;
   // workgroups go to the 8 XCDs in turn: give each XCD a contiguous run of items, so the four items of a 64-row record
   // block (and their shared 128-byte lines of scale words) meet in one L2 instead of four
@@ -498,49 +508,58 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
   const uint32_t nB = item * (uint32_t)SN_ROWS;
   const uint32_t wsc = glu ? (ri < 8 ? 2u * ri : 2u * (ri - 8) + 1u) : (uint32_t)ri;
   const uint32_t r = wrow(p, nB + wsc);
-  const uint32_t nun = p.K / UK;                               // units (32 k) of the call
-  const uint32_t woff = ((r >> 6) * p.wG + (p.wk0 >> 5)) * 1280u + (r & 63u) * 16u;
-  const uint32_t sadj = 1024u - (r & 63u) * 12u;             // code row -> scale word of row r in the record
+  const uint32_t nun = p.K / UK;                               // units of the call
+  // byte offset of row r's first unit and of its scale word from a unit's code row (q4: scale word r at 1024 + 4 r;
+  // q8: the f16 scale of row r at 4096 + 2 r, read as the 4-byte word of its row pair)
+  constexpr uint32_t USTRIDE = WE == W_Q4 ? 1280u : 4224u;
+  const uint32_t woff = WE == W_Q4 ? ((r >> 6) * p.wG + (p.wk0 >> 5)) * 1280u + (r & 63u) * 16u
+                                   : ((r >> 6) * p.wG + (p.wk0 >> 6)) * 4224u + (r & 63u) * 64u;
+  const uint32_t sadj = WE == W_Q4 ? 1024u - (r & 63u) * 12u : 4096u - (r & 63u) * 64u + (r & 62u) * 2u;
   const srsrc wr = stream_rsrc(p.W);
   // this thread's first chunk of X before the weights (loads return in issue order: issued after them, it would wait
   // for the whole item's weights before the staging below could start)
-  const uint32_t nb = p.K / 8, nx = MT * nb;                   // 8-k chunks (nx is a multiple of 4: whole lane quads)
+  const uint32_t nb = p.K / 8, nx = MT * nb;                   // 8-k chunks (nx is a multiple of CPU_: whole lane groups)
   u32x4 xv0 = (u32x4){0u, 0u, 0u, 0u};
   if ((uint32_t)tid < nx && (uint32_t)tid / nb < p.M) xv0 = xload8<XM>(p, tid / nb, RowCtx{0, 0, 0}, 8 * (tid % nb));
   __builtin_amdgcn_sched_barrier(0);
-  // every weight load of this lane (clamped past the last unit: the clamped ones are not reduced)
-  u32x4 code[RND];
-  uint32_t sm[RND];
+  // every weight load of this lane (clamped past the last unit: the clamped ones are not reduced); q4: its unit's code
+  // row and scale word; q8: its chunk of each of the round's four units (unit 4 w + c in code[rd][c]) and their scales
+  u32x4 code[RND][NC];
+  uint32_t sm[RND][NC];
 #pragma unroll
   for (int rd = 0; rd < RND; rd++) {
-    uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)us;
-    u = u < nun ? u : nun - 1u;
-    code[rd] = sload128(wr, woff + u * 1280u);
-    sm[rd] = sload32(wr, woff + u * 1280u + sadj);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)(WE == W_Q8 ? c : us);
+      u = u < nun ? u : nun - 1u;
+      code[rd][c] = sload128(wr, woff + u * USTRIDE + (WE == W_Q8 ? 16u * (uint32_t)us : 0u));
+      sm[rd][c] = sload32(wr, woff + u * USTRIDE + sadj);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // X' -> LDS in the pair order of the encoding, and per unit and row the X' sums over the low / high nibble positions
+  // X' -> LDS in the pair order of the encoding, and per unit and row the X' sums (q4: over the low / high nibble
+  // positions; q8: the whole unit, in .x)
   extern __shared__ __attribute__((aligned(16))) uint8_t sn_smem[];
   f16 *sX = (f16 *)sn_smem;                                    // [MT][K]
-  f32x2 *sG = (f32x2 *)(sn_smem + (size_t)MT * p.K * 2);      // [MT][K / 32]
-  for (uint32_t t = tid; t < (nx + 3u) / 4u * 4u; t += SN_NT) {
+  f32x2 *sG = (f32x2 *)(sn_smem + (size_t)MT * p.K * 2);      // [MT][K / UK]
+  for (uint32_t t = tid; t < nx; t += SN_NT) {
     const uint32_t m = t / nb, kq = t - m * nb;
     u32x4 v = (u32x4){0u, 0u, 0u, 0u};
     if (t == (uint32_t)tid) v = xv0;
-    else if (t < nx && m < p.M) v = xload8<XM>(p, m, RowCtx{0, 0, 0}, 8 * kq);
-    v = xperm<W_Q4>(v);
+    else if (m < p.M) v = xload8<XM>(p, m, RowCtx{0, 0, 0}, 8 * kq);
+    v = xperm<WE>(v);
     const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
     float lo = __builtin_amdgcn_fdot2(as_h2(v.z), one2, __builtin_amdgcn_fdot2(as_h2(v.x), one2, 0.0f, false), false);
     float hi = __builtin_amdgcn_fdot2(as_h2(v.w), one2, __builtin_amdgcn_fdot2(as_h2(v.y), one2, 0.0f, false), false);
+    if constexpr (WE == W_Q8) { lo += hi; hi = 0.0f; }
     lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0xB1, 0xF, 0xF, false));
     hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0xB1, 0xF, 0xF, false));
     lo += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, lo), 0x4E, 0xF, 0xF, false));
     hi += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, hi), 0x4E, 0xF, 0xF, false));
-    if (t < nx) {
-      if (kq % 4u == 0u) sG[m * (nb / 4u) + kq / 4u] = (f32x2){lo, hi};
-      *(u32x4 *)(sX + (size_t)m * p.K + 8 * kq) = v;
-    }
+    if constexpr (CPU_ == 8) lo += __shfl_xor(lo, 4);         // q8: a unit's 8 chunks are two lane quads
+    if (kq % CPU_ == 0u) sG[m * (nb / CPU_) + kq / CPU_] = (f32x2){lo, hi};
+    *(u32x4 *)(sX + (size_t)m * p.K + 8 * kq) = v;
   }
   __syncthreads();
 
@@ -551,43 +570,85 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
   for (int m = 0; m < MT; m++) acc[m] = 0.0f;
 #pragma unroll
   for (int rd = 0; rd < RND; rd++) {
-    const uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)us;
-    if (u >= nun) break;                                       // (units ascend with rd)
-    const uint32_t wd[4] = {code[rd].x, code[rd].y, code[rd].z, code[rd].w};
-    uint32_t h[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t w8 = wd[i] >> 8;
-      h[4 * i + 0] = (wd[i] & mlo) | mag;
-      h[4 * i + 1] = (wd[i] & mhi) | mag;
-      h[4 * i + 2] = (w8 & mlo) | mag;
-      h[4 * i + 3] = (w8 & mhi) | mag;
-    }
-    const f16x2 sm2 = as_h2(sm[rd]);
-    const float s = (float)sm2.x, mn = (float)sm2.y;
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-      const u32x4 *x4 = (const u32x4 *)(sX + (size_t)m * p.K + u * UK);
-      float dlo = 0.0f, dhi = 0.0f;
+    if constexpr (WE == W_Q4) {
+      const uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)us;
+      if (u >= nun) break;                                     // (units ascend with rd)
+      const uint32_t wd[4] = {code[rd][0].x, code[rd][0].y, code[rd][0].z, code[rd][0].w};
+      uint32_t h[16];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const u32x4 xv = x4[i];
-        dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), dlo, false);
-        dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), dhi, false);
-        dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), dlo, false);
-        dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), dhi, false);
+        const uint32_t w8 = wd[i] >> 8;
+        h[4 * i + 0] = (wd[i] & mlo) | mag;
+        h[4 * i + 1] = (wd[i] & mhi) | mag;
+        h[4 * i + 2] = (w8 & mlo) | mag;
+        h[4 * i + 3] = (w8 & mhi) | mag;
       }
-      const f32x2 g = sG[m * (nb / 4u) + u];
-      const float t = fmaf(-1024.0f, g.x, dlo) + 0.0625f * fmaf(-1024.0f, g.y, dhi);   // sum x q, exact for e_k
-      acc[m] = fmaf(s, t, fmaf(mn, g.x + g.y, acc[m]));
+      const f16x2 sm2 = as_h2(sm[rd][0]);
+      const float s = (float)sm2.x, mn = (float)sm2.y;
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const u32x4 *x4 = (const u32x4 *)(sX + (size_t)m * p.K + u * UK);
+        float dlo = 0.0f, dhi = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const u32x4 xv = x4[i];
+          dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), dlo, false);
+          dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), dhi, false);
+          dlo = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), dlo, false);
+          dhi = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), dhi, false);
+        }
+        const f32x2 g = sG[m * (nb / 4u) + u];
+        const float t = fmaf(-1024.0f, g.x, dlo) + 0.0625f * fmaf(-1024.0f, g.y, dhi);   // sum x q, exact for e_k
+        acc[m] = fmaf(s, t, fmaf(mn, g.x + g.y, acc[m]));
+      }
+    } else {
+      // q8: (1152 + q) in the fp16 halves (the code byte's sign bit flipped puts 128 + q in the low byte), one FMA
+      // removes 1152 X, and the row's scale multiplies the unit's sum, as in k_gemv; the lane holds 16 k of the unit
+      // (chunk us), and the chunk-0 lane removes the unit's 1152 X for all four
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const uint32_t u = (uint32_t)rd * 32u + (uint32_t)wave * 4u + (uint32_t)c;
+        if (u >= nun) break;                                   // (units ascend with c and rd)
+        uint32_t h[8];
+        const uint32_t wd[4] = {code[rd][c].x ^ 0x80808080u, code[rd][c].y ^ 0x80808080u, code[rd][c].z ^ 0x80808080u,
+                                code[rd][c].w ^ 0x80808080u};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          h[2 * j + 0] = perm(0x64646464u, wd[j], 0x04020400u);   // (1152 + q0, 1152 + q2)
+          h[2 * j + 1] = perm(0x64646464u, wd[j], 0x04030401u);   // (1152 + q1, 1152 + q3)
+        }
+        const uint32_t sh = (r & 1u) ? (sm[rd][c] >> 16) : (sm[rd][c] & 0xffffu);
+        const float s = (float)__builtin_bit_cast(f16, (uint16_t)sh);
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          const u32x4 *x4 = (const u32x4 *)(sX + (size_t)m * p.K + u * UK + 16u * (uint32_t)us);
+          float d = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 2; i++) {
+            const u32x4 xv = x4[i];
+            d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 0]), as_h2(xv.x), d, false);
+            d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 1]), as_h2(xv.y), d, false);
+            d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 2]), as_h2(xv.z), d, false);
+            d = __builtin_amdgcn_fdot2(as_h2(h[4 * i + 3]), as_h2(xv.w), d, false);
+          }
+          const float g = us == 0 ? sG[m * (nb / 8u) + u].x : 0.0f;
+          acc[m] = fmaf(s, fmaf(-1152.0f, g, d), acc[m]);
+        }
+      }
     }
   }
-  // the row's four lanes (l, l + 16, l + 32, l + 48) in a fixed order, then the waves in wave order
+  // the row's four lanes (q4: l, l + 16, l + 32, l + 48; q8: a lane quad) in a fixed order, then the waves in wave
+  // order
   float *sR = (float *)sn_smem;                                // [wave][MT][16] after a barrier (X' is dead)
 #pragma unroll
   for (int m = 0; m < MT; m++) {
-    acc[m] += __shfl_xor(acc[m], 16);
-    acc[m] += __shfl_xor(acc[m], 32);
+    if constexpr (WE == W_Q8) {
+      acc[m] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc[m]), 0xB1, 0xF, 0xF, false));
+      acc[m] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc[m]), 0x4E, 0xF, 0xF, false));
+    } else {
+      acc[m] += __shfl_xor(acc[m], 16);
+      acc[m] += __shfl_xor(acc[m], 32);
+    }
   }
   __syncthreads();
   if (us == 0) {
@@ -637,44 +698,57 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
   }
 }
 
-// rounds of 32 units (1024 k) a short-call item takes, the longest K it serves and its LDS bytes
-constexpr int SN_RND_MAX = 16;
-unsigned gemv_sn_kmax() { return SN_RND_MAX * 32u * 32u; }
+// the longest K a short-call item serves (rounds of 32 units: q4 up to 16 of 1024 k, q8 up to 4 of 2048 k, whose
+// four code loads per unit take 16 registers per round) and its LDS bytes
+constexpr int SN_RND_Q4 = 16, SN_RND_Q8 = 4;
+unsigned gemv_sn_kmax(int we) { return we == W_Q8 ? SN_RND_Q8 * 32u * 64u : SN_RND_Q4 * 32u * 32u; }
 // X' and its per-unit sums; after the stream the same buffer holds the waves' partials (8 waves x M x 16 floats)
-static uint32_t sn_lds(uint32_t M, uint32_t K) {
-  const uint32_t x = M * K * 2u + M * (K / 32u) * 8u, r = (uint32_t)(SN_NT / 64) * M * SN_ROWS * 4u;
+uint32_t gemv_sn_lds(int we, uint32_t M, uint32_t K) {
+  const uint32_t x = M * K * 2u + M * (K / (we == W_Q8 ? 64u : 32u)) * 8u, r = (uint32_t)(SN_NT / 64) * M * SN_ROWS * 4u;
   return x > r ? x : r;
 }
 
-template <int XM, int MT>
+template <int WE, int XM, int MT>
 static hipError_t launch_sn_mt(const Params &p, hipStream_t s) {
-  const uint32_t rounds = (p.K / 32u + 31u) / 32u;
-  const uint32_t lds = sn_lds(MT, p.K);
+  const uint32_t rounds = (p.K / (uint32_t)SnUnit<WE>::UK + 31u) / 32u;
+  const uint32_t lds = gemv_sn_lds(WE, MT, p.K);
   const dim3 grid((p.N + SN_ROWS - 1) / SN_ROWS);
-#define SN_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn<XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
-  switch (rounds <= 4 ? 4 : rounds <= 8 ? 8 : rounds <= 12 ? 12 : 16) {
-    SN_CASE(4) SN_CASE(8) SN_CASE(12) SN_CASE(16)
-  default: return hipErrorInvalidValue;
+#define SN_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn<WE, XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
+  if constexpr (WE == W_Q4) {
+    switch (rounds <= 4 ? 4 : rounds <= 8 ? 8 : rounds <= 12 ? 12 : 16) {
+      SN_CASE(4) SN_CASE(8) SN_CASE(12) SN_CASE(16)
+    default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (rounds <= 2 ? 2 : 4) {
+      SN_CASE(2) SN_CASE(4)
+    default: return hipErrorInvalidValue;
+    }
   }
 #undef SN_CASE
   return hipGetLastError();
 }
-template <int XM>
+template <int WE, int XM>
 static hipError_t launch_sn_x(const Params &p, hipStream_t s) {
-  if (p.M == 1) return launch_sn_mt<XM, 1>(p, s);
-  if (p.M == 2) return launch_sn_mt<XM, 2>(p, s);
-  return launch_sn_mt<XM, 4>(p, s);
+  if (p.M == 1) return launch_sn_mt<WE, XM, 1>(p, s);
+  if (p.M == 2) return launch_sn_mt<WE, XM, 2>(p, s);
+  return launch_sn_mt<WE, XM, 4>(p, s);
 }
-hipError_t launch_gemv_sn(const Params &p, int xm, hipStream_t s) {
-  if (p.M == 0 || p.M > 4 || p.K % 32 || p.K > gemv_sn_kmax() || p.wk0 % 32 || p.epi == E_HEADS ||
-      p.epi == E_ONORMGATE || sn_lds(p.M <= 2 ? p.M : 4, p.K) > 64u * 1024u)
-    return hipErrorInvalidValue;
+template <int WE>
+static hipError_t launch_sn_w(const Params &p, int xm, hipStream_t s) {
   switch (xm) {
-  case X_F16: return launch_sn_x<X_F16>(p, s);
-  case X_LNMOD: return launch_sn_x<X_LNMOD>(p, s);
-  case X_RMS: return launch_sn_x<X_RMS>(p, s);
+  case X_F16: return launch_sn_x<WE, X_F16>(p, s);
+  case X_LNMOD: return launch_sn_x<WE, X_LNMOD>(p, s);
+  case X_RMS: return launch_sn_x<WE, X_RMS>(p, s);
   }
   return hipErrorInvalidValue;
+}
+hipError_t launch_gemv_sn(const Params &p, int we, int xm, hipStream_t s) {
+  const uint32_t uk = we == W_Q8 ? 64u : 32u;
+  if ((we != W_Q4 && we != W_Q8) || p.M == 0 || p.M > 4 || p.K % uk || p.K > gemv_sn_kmax(we) || p.wk0 % uk ||
+      p.epi == E_HEADS || p.epi == E_ONORMGATE || gemv_sn_lds(we, p.M <= 2 ? p.M : 4, p.K) > 64u * 1024u)
+    return hipErrorInvalidValue;
+  return we == W_Q4 ? launch_sn_w<W_Q4>(p, xm, s) : launch_sn_w<W_Q8>(p, xm, s);
 }
 
 // ------------------------------------------------------------------------------------------------------------------

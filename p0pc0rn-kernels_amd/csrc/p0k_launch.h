@@ -35,10 +35,11 @@ unsigned gemv_ks_max(unsigned M, int we, bool mf, bool mx);   // longest K slice
 unsigned gemv_unit_k(int we, bool mf);                      // k of one decode weight unit
 hipError_t launch_gemv(const Params &p, int we, int xm, float *part, unsigned *cnt, unsigned S, unsigned KS, hipStream_t s,
                        bool mf, bool mq4, bool mx, bool narrow);
-// short decode calls: q4, 1..4 rows, element-wise epilogues, K % 32 == 0 and K <= gemv_sn_kmax(); items of 16 weight
-// rows with no K split (ceil(N / 16) workgroups)
-unsigned gemv_sn_kmax();
-hipError_t launch_gemv_sn(const Params &p, int xm, hipStream_t s);
+// short decode calls: q4 or q8, 1..4 rows, element-wise epilogues, K a multiple of the unit (32 / 64) and at most
+// gemv_sn_kmax(we), LDS (gemv_sn_lds) at most 64 KB; items of 16 weight rows with no K split (ceil(N / 16) workgroups)
+unsigned gemv_sn_kmax(int we);
+unsigned gemv_sn_lds(int we, unsigned M, unsigned K);
+hipError_t launch_gemv_sn(const Params &p, int we, int xm, hipStream_t s);
 // rowstats (src/ops/misc.js:16-44)
 hipError_t launch_rowstats(const void *x, unsigned ld, unsigned c0, unsigned rows, unsigned cols, int mode, float eps,
                            float *st, unsigned st_off, hipStream_t s);

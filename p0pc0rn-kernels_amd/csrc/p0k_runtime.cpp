@@ -523,7 +523,7 @@ static int gemm_run(p0k_ctx *c, const p0k_gemm_args *a, WsSource ws) {
   HIPCHK(hipSetDevice(c->device), "hipSetDevice");
   hipError_t e;
   if (plan.kernel == p0k::K_GEMV_SN) {
-    e = p0k::launch_gemv_sn(p, plan.xm, c->stream);
+    e = p0k::launch_gemv_sn(p, plan.we, plan.xm, c->stream);
   } else if (plan.kernel == p0k::K_GEMV || plan.kernel == p0k::K_GEMV_MF) {
     const uint32_t tiles = (a->N + 127) / 128;
     float *part = nullptr;

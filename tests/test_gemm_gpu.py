@@ -103,16 +103,16 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    short = M <= 2 and enc.startswith("q4") and epi not in ("heads", "onormgate")
+    short = (M <= 2 if enc.startswith("q4") else M <= 4 and enc.startswith("q8")) and epi not in ("heads", "onormgate")
     assert kern == ("gemv_short" if short else "gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else
                     "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
     if short:
-        # the one-row / 2-row stream kernel on the same call (P0K_GEMV_SN=0)
+        # the one-row / 2-row stream kernel (q4) or the matrix-core decode (q8) on the same call (P0K_GEMV_SN=0)
         monkeypatch.setenv("P0K_GEMV_SN", "0")
-        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv"
+        assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if enc.startswith("q4") else "gemv_mfma")
         got = c.run_device(dev)
         assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M} stream")
     if kern == "mfma_dma":
@@ -246,6 +246,7 @@ def test_narrow_matrix_core_decode(dev, enc, epi, M, N, K, mq4, narrow, monkeypa
     oracle's CPU weight model, ragged last items and unaligned N included."""
     monkeypatch.setenv("P0K_GEMV_NARROW", "1" if narrow else "0")
     monkeypatch.setenv("P0K_GEMV_MQ4", mq4)
+    monkeypatch.setenv("P0K_GEMV_SN", "0")                  # (q8 N 14336 at one row would take the 16-row items)
     banner(f"narrow={narrow} {enc} {epi} M={M} N={N} K={K} mq4={mq4}")
     c = make_case(enc=enc, epi=epi, M=M, N=N, K=K, seed=93)
     t = dev.select_tile(c.args(lambda n: c.bufs[n]))
@@ -283,8 +284,8 @@ def test_dequant_bit_exact(dev, enc, path, monkeypatch):
     to exercise both decoder paths. (q8 at M = 1 takes the matrix-core GEMV; P0K_GEMV_MF=0 keeps the VALU stream;
     P0K_GEMV_MX=16 the stream kernel's 4x4x4 matrix-core form for q4 with 2..16 rows; P0K_GEMV_MQ4=0 the q4
     matrix-core decode with X' staged in LDS.)"""
-    if (path.startswith("gemv_mx") or path.startswith("gemv_short")) and not enc.startswith("q4"):
-        pytest.skip("the stream kernel's matrix-core form and the short-call kernel are q4 only")
+    if path.startswith("gemv_mx") and not enc.startswith("q4"):
+        pytest.skip("the stream kernel's matrix-core form is q4 only")
     monkeypatch.setenv("P0K_GEMV_SN", "1" if path.startswith("gemv_short") else "0")
     if path == "gemv":
         monkeypatch.setenv("P0K_GEMV_MF", "0")
@@ -700,6 +701,36 @@ def test_short_decode_matches_oracle(dev, kw, monkeypatch):
     assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short {kw}")
+
+
+SHORT_CASES_Q8 = [
+    dict(M=1, N=4096, K=4096, epi="f16"),
+    dict(M=2, N=136, K=128, epi="f32"),
+    dict(M=4, N=40, K=64, epi="f16"),           # one unit: the partials need more LDS than X' does
+    dict(M=3, N=24, K=1088, epi="bias", bias=True, res=True),
+    dict(M=1, N=520, K=8192, epi="resadd", gate=True, bias=True),
+    dict(M=4, N=1024, K=4096, epi="resadd", gate=True, bias=True),
+    dict(M=1, N=512, K=2048, epi="swiglu", bias=True),
+    dict(M=2, N=272, K=3072, epi="swiglu", act="gelu"),
+    dict(M=1, N=256, K=512, epi="resadd", store=True, xmode="rms"),
+    dict(M=2, N=128, K=1024, epi="f16", xmode="lnmod"),
+    dict(M=1, N=200, K=256, epi="f16", ld_pad=8, k0=64, wk0=64, n0=8),
+    dict(M=2, N=96, K=192, epi="swiglu", wr0=64, ld_pad=16),
+]
+
+
+@pytest.mark.parametrize("kw", SHORT_CASES_Q8, ids=lambda k: f"M{k['M']}-N{k['N']}-K{k['K']}-{k.get('xmode', 'f16')}-{k['epi']}")
+def test_short_decode_q8_matches_oracle(dev, kw, monkeypatch):
+    """The short-call decode with q8 weights (64-k units, four 16-byte code loads each; P0K_GEMV_SN=1 forces it): 1..4
+    rows, K from one unit to its longest (8192), K not a multiple of the 2048-k round, N not a multiple of the item,
+    the element-wise epilogues, rms / lnmod, offsets; against the oracle's CPU weight model."""
+    monkeypatch.setenv("P0K_GEMV_SN", "1")
+    kw = dict(kw)
+    c = make_case(enc="q8g64s.t64", seed=71 + kw["K"] % 89, wscale=0.02, **kw)
+    banner(f"short decode q8 {kw}")
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short q8 {kw}")
 
 
 def test_caller_captured_stream_keeps_its_workspace(dev):

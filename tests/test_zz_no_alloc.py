@@ -34,7 +34,8 @@ PAIRS = {
 
 
 @pytest.mark.parametrize("name", list(PAIRS))
-def test_noalloc_matches_gemm(dev, name):
+def test_noalloc_matches_gemm(dev, name, monkeypatch):
+    monkeypatch.setenv("P0K_GEMV_SN", "0")                  # the split decode, not the 16-row items (no workspace)
     for i, kw in enumerate(PAIRS[name]):
         print(f"[no-alloc] {name} call {i} {kw}", flush=True)
         c = make_case(**kw)
