@@ -81,16 +81,17 @@ Tuning tuning_from_env(unsigned cus) {
 // M 2 6.06 vs 6.89, M 4 7.92 vs 7.35; N 6144 M 1 6.02 vs 6.43, M 2 7.77 vs 7.08; N 14336 M 1 9.71 vs 7.98; N 4096
 // K 8192 M 1 7.81 vs 9.98; K 14336 12.0 vs 11.9; SwiGLU out 4096 (8192 weight rows) M 1 7.91 vs 7.57. (A plain
 // one-launch read of the same 10.5 MB as N 4096 K 4096 takes 4.3-4.5 us: the short calls are latency, not bytes.)
-// q8 (against the matrix-core decode): every q8 call with up to 3.5 items per CU at one row, 2 at two rows and 1 at
-// 3..4 rows, K up to 8192 (all that fits): plain N 4096 K 4096 M 1 / 2 / 4 5.21 / 6.67 / 8.57 vs 9.58 / 9.71 / 9.95 us;
+// q8 (against the matrix-core decode): every q8 call at one row, with up to 2 items per CU at two rows and 1 at 3..4
+// rows, K up to 8192 (all that fits): plain N 4096 K 4096 M 1 / 2 / 4 5.21 / 6.67 / 8.57 vs 9.58 / 9.71 / 9.95 us;
 // N 2048 4.44 / 5.91 / 7.68 vs 9.34 / 9.50 / 9.70; K 2048 4.12 / 4.76 / 5.88 vs 6.99 / 7.10 / 7.28; N 8192 M 1 / 2
 // 7.48 / 9.68 vs 10.16 / 10.25 (M 4 13.17 vs 10.49); N 14336 M 1 11.93 vs 12.69 (M 2 15.13 vs 12.59); N 4096 K 8192
 // M 1 / 2 9.47 / 11.31 vs 13.56 / 13.71; SwiGLU out 4096 M 1 / 2 7.64 / 9.66 vs 11.69 / 11.74, out 7168 M 1 12.15 vs
-// 13.93; N 6144 M 4 11.95 vs 10.29, N 10240 M 2 11.64 vs 10.71 (not taken).
+// 13.93, out 14336 (28672 weight rows, 121 MB) 20.79 vs 22.43; N 20480 / 28672 M 1 15.85 / 20.28 vs 20.90 / 22.43;
+// N 6144 M 4 11.95 vs 10.29, N 10240 M 2 11.64 vs 10.71, N 28672 M 2 24.96 vs 22.57 (not taken).
 static bool sn_rule(int we, uint32_t N, uint32_t K, uint32_t M, unsigned cus) {
   const uint64_t items = (N + 15u) / 16u;
   if (we == P0K_ENC_Q8G64S_T64)
-    return K <= 8192u && (M == 1 ? items * 2u <= (uint64_t)cus * 7u : M == 2 ? items <= (uint64_t)cus * 2u : items <= cus);
+    return K <= 8192u && (M == 1 || (M == 2 ? items <= (uint64_t)cus * 2u : items <= cus));
   return M <= 2 && K <= 8192u && items * 2u <= (uint64_t)cus * (M == 1 ? 3u : 2u);
 }
 

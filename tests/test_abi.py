@@ -232,8 +232,8 @@ def test_decode_row_routing_switch(monkeypatch):
 
 def test_short_decode_routing(monkeypatch):
     """q4 decode with one or two rows whose 16-row items number at most about one per CU (1.5 per CU at one row), K up to
-    8192 and an element-wise epilogue takes the short-call kernel; q8 decode with up to 3.5 / 2 / 1 items per CU at
-    1 / 2 / 3..4 rows and K up to 8192 as well; P0K_GEMV_SN=0 / 1 switch it off / on wherever it can run (up to 4
+    8192 and an element-wise epilogue takes the short-call kernel; q8 decode at one row, and with up to 2 / 1 items per CU at
+    2 / 3..4 rows and K up to 8192 as well; P0K_GEMV_SN=0 / 1 switch it off / on wherever it can run (up to 4
     rows, K up to 16384 for q4 and 8192 for q8, X' in 64 KB of LDS); f16 weights never take it."""
     q4 = lambda M, N, K, **kw: p0k.select_tile(host_args(make_case(M=M, enc="q4g32a.t64", N=N, K=K, **kw)))["kernel"]   # noqa: E731
     assert q4(1, 4096, 4096) == "gemv_short" and q4(2, 4096, 4096) == "gemv_short"
@@ -245,7 +245,7 @@ def test_short_decode_routing(monkeypatch):
     assert q8(1, 256, 512) == "gemv_short" and q8(1, 14336, 4096) == "gemv_short" and q8(2, 8192, 4096) == "gemv_short"
     assert q8(4, 4096, 4096) == "gemv_short" and q8(1, 4096, 8192) == "gemv_short"
     assert q8(2, 10240, 4096) == "gemv_mfma" and q8(4, 6144, 4096) == "gemv_mfma" and q8(1, 4096, 8704) != "gemv_short"
-    assert q8(1, 28672, 4096) == "gemv_mfma"                                              # 1792 items: 7 per CU
+    assert q8(1, 28672, 4096) == "gemv_short" and q8(2, 28672, 4096) == "gemv_mfma"   # 1792 items: 7 per CU
     assert p0k.select_tile(host_args(make_case(M=1, enc="f16", N=256, K=512)))["kernel"] == "gemv_mfma"
     monkeypatch.setenv("P0K_GEMV_SN", "0")
     assert q4(1, 4096, 4096) == "gemv" and q8(1, 4096, 4096) == "gemv_mfma"
