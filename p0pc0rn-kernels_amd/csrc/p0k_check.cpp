@@ -88,8 +88,14 @@ Tuning tuning_from_env(unsigned cus) {
 // M 1 / 2 9.47 / 11.31 vs 13.56 / 13.71; SwiGLU out 4096 M 1 / 2 7.64 / 9.66 vs 11.69 / 11.74, out 7168 M 1 12.15 vs
 // 13.93, out 14336 (28672 weight rows, 121 MB) 20.79 vs 22.43; N 20480 / 28672 M 1 15.85 / 20.28 vs 20.90 / 22.43;
 // N 6144 M 4 11.95 vs 10.29, N 10240 M 2 11.64 vs 10.71, N 28672 M 2 24.96 vs 22.57 (not taken).
+// f16 (16-byte rows; against the matrix-core decode): every call with 1..4 rows and K up to 8192: N 4096 K 4096 M 1 / 2
+// / 4 6.97 / 7.96 / 9.42 vs 14.21 / 14.31 / 14.38 us; N 2048 5.28 / 6.20 / 7.57 vs 14.43 / 15.26 / 15.34; N 8192
+// 11.55 / 12.69 / 15.05 vs 29.63 / 29.71 / 29.94; N 14336 K 2048 10.89 / 11.21 / 12.68 vs 21.99 / 22.10 / 22.35; N 14336
+// K 4096 19.09 / 20.30 / 24.94 vs 28.35 / 28.57 / 28.95; N 4096 K 8192 12.87 / 14.14 / 16.78 vs 26.92 / 27.16 / 27.37;
+// SwiGLU out 7168 19.43 / 20.46 / 25.33 vs 30.26 / 29.54 / 29.75.
 static bool sn_rule(int we, uint32_t N, uint32_t K, uint32_t M, unsigned cus) {
   const uint64_t items = (N + 15u) / 16u;
+  if (we == P0K_ENC_F16) return true;
   if (we == P0K_ENC_Q8G64S_T64)
     return K <= 8192u && (M == 1 || (M == 2 ? items <= (uint64_t)cus * 2u : items <= cus));
   return M <= 2 && K <= 8192u && items * 2u <= (uint64_t)cus * (M == 1 ? 3u : 2u);
@@ -321,11 +327,11 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
         if (K % (s2 * quant) == 0 && K / s2 <= gemv_ks_max(M, we, mf, mx)) { S = s2; KS = K / s2; }
       }
       if (S) kernel = mf ? K_GEMV_MF : K_GEMV;
-      // short calls (q4 or q8, up to 4 rows, element-wise epilogues): 16-row items, no K split, every load of an item
+      // short calls (q4, q8, or f16 with 16-byte rows; up to 4 rows, element-wise epilogues): 16-row items, no K split, every load of an item
       // in flight at once (sn_rule above)
-      const uint32_t snuk = we == P0K_ENC_Q8G64S_T64 ? 64u : 32u;
-      const bool sn_ok = (we == P0K_ENC_Q4G32A_T64 || we == P0K_ENC_Q8G64S_T64) && M <= 4 && epi != P0K_EPI_HEADS &&
-                         epi != P0K_EPI_ONORMGATE && K % snuk == 0 && K <= gemv_sn_kmax(we) && a->wk0 % snuk == 0 &&
+      const uint32_t snuk = we == P0K_ENC_Q4G32A_T64 ? 32u : 64u, snwk = we == P0K_ENC_F16 ? 8u : snuk;
+      const bool sn_ok = (we != P0K_ENC_F16 || (f & F_WALIGN8)) && M <= 4 && epi != P0K_EPI_HEADS &&
+                         epi != P0K_EPI_ONORMGATE && K % snuk == 0 && K <= gemv_sn_kmax(we) && a->wk0 % snwk == 0 &&
                          gemv_sn_lds(we, M <= 2 ? M : 4, K) <= 64u * 1024u;
       if (sn_ok && (tune.gemv_sn == 1 || (tune.gemv_sn < 0 && sn_rule(we, N, K, M, tune.cus)))) {
         kernel = K_GEMV_SN;

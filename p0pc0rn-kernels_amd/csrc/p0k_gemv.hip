@@ -495,6 +495,53 @@ struct SnUnit<W_Q4> { static constexpr int UK = 32, NC = 1; };
 template <>
 struct SnUnit<W_Q8> { static constexpr int UK = 64, NC = 4; };
 
+// the epilogue of a short-call item: sR[wave][MT][16] holds each wave's sums of the item's 16 ws columns; the waves
+// are added in wave order and one thread per output element applies the element-wise epilogue
+template <int MT>
+__device__ __forceinline__ void sn_epilogue(const Params &p, const float *sR, uint32_t nB, int tid) {
+  const bool glu = p.epi == E_SWIGLU;
+  const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
+  auto tot = [&](uint32_t m, uint32_t i) {
+    float v = sR[m * SN_ROWS + i];
+#pragma unroll
+    for (int w = 1; w < SN_NT / 64; w++) v += sR[(w * MT + m) * SN_ROWS + i];
+    return v;
+  };
+  if (glu) {                                                                      // gemm.js:204-210
+    const uint32_t Nout = p.N >> 1;
+    const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
+    if ((uint32_t)tid < rows * 8u) {
+      const uint32_t m = tid / 8, c = tid % 8, o = (nB >> 1) + c;
+      if (o < Nout) {
+        float gt = tot(m, c), u = tot(m, 8 + c);
+        if (bias) { gt += p.BV[p.bvOff + o]; u += p.BV[p.bvOff + p.bvUp + o]; }
+        ((uint16_t *)p.Y)[(size_t)m * p.ldy + p.ny0 + o] = h_bits(glu_act(gt, gelu) * u);
+      }
+    }
+    return;
+  }
+  if ((uint32_t)tid < rows * SN_ROWS) {
+    const uint32_t m = tid / SN_ROWS, c = tid % SN_ROWS, col = nB + c;
+    if (col >= p.N) return;
+    const float v = tot(m, c);
+    const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
+    if (p.epi == E_F16) {                                                         // gemm.js:194-196
+      ((uint16_t *)p.Y)[yi] = h_bits(v);
+    } else if (p.epi == E_F32) {
+      ((float *)p.Y)[yi] = v;
+    } else if (p.epi == E_BIAS) {                                                 // gemm.js:211-215
+      float rr = v + p.EV[p.evOff + col];
+      if (p.flags & F_RES) rr += h_val(((const uint16_t *)p.Y)[yi]);
+      ((uint16_t *)p.Y)[yi] = h_bits(rr);
+    } else {                                                                      // resadd, gemm.js:197-203
+      const float g = (p.flags & F_GATE) ? p.EV[p.evOff + col] : 1.0f;
+      const float b = (p.flags & F_BIAS) ? p.BV[p.bvOff + col] : 0.0f;
+      float *y = (float *)p.Y + yi;
+      *y = ((p.flags & F_STORE) ? 0.0f : *y) + g * (v + b);
+    }
+  }
+}
+
 template <int WE, int XM, int MT, int RND>
 __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
   constexpr int UK = SnUnit<WE>::UK, NC = SnUnit<WE>::NC, CPU_ = UK / 8;   // k per unit, code loads, 8-k chunks
@@ -656,77 +703,152 @@ __global__ __launch_bounds__(SN_NT) void k_gemv_sn(Params p) {
     for (int m = 0; m < MT; m++) sR[(wave * MT + m) * SN_ROWS + ri] = acc[m];
   }
   __syncthreads();
-  const uint32_t rows = p.M < (uint32_t)MT ? p.M : (uint32_t)MT;
-  auto tot = [&](uint32_t m, uint32_t i) {
-    float v = sR[m * SN_ROWS + i];
-#pragma unroll
-    for (int w = 1; w < SN_NT / 64; w++) v += sR[(w * MT + m) * SN_ROWS + i];
-    return v;
-  };
-  if (glu) {                                                                      // gemm.js:204-210
-    const uint32_t Nout = p.N >> 1;
-    const bool bias = p.flags & F_BIAS, gelu = p.flags & F_GELU;
-    if ((uint32_t)tid < rows * 8u) {
-      const uint32_t m = tid / 8, c = tid % 8, o = (nB >> 1) + c;
-      if (o < Nout) {
-        float gt = tot(m, c), u = tot(m, 8 + c);
-        if (bias) { gt += p.BV[p.bvOff + o]; u += p.BV[p.bvOff + p.bvUp + o]; }
-        ((uint16_t *)p.Y)[(size_t)m * p.ldy + p.ny0 + o] = h_bits(glu_act(gt, gelu) * u);
-      }
-    }
-    return;
-  }
-  if ((uint32_t)tid < rows * SN_ROWS) {
-    const uint32_t m = tid / SN_ROWS, c = tid % SN_ROWS, col = nB + c;
-    if (col >= p.N) return;
-    const float v = tot(m, c);
-    const size_t yi = (size_t)m * p.ldy + p.ny0 + col;
-    if (p.epi == E_F16) {                                                         // gemm.js:194-196
-      ((uint16_t *)p.Y)[yi] = h_bits(v);
-    } else if (p.epi == E_F32) {
-      ((float *)p.Y)[yi] = v;
-    } else if (p.epi == E_BIAS) {                                                 // gemm.js:211-215
-      float rr = v + p.EV[p.evOff + col];
-      if (p.flags & F_RES) rr += h_val(((const uint16_t *)p.Y)[yi]);
-      ((uint16_t *)p.Y)[yi] = h_bits(rr);
-    } else {                                                                      // resadd, gemm.js:197-203
-      const float g = (p.flags & F_GATE) ? p.EV[p.evOff + col] : 1.0f;
-      const float b = (p.flags & F_BIAS) ? p.BV[p.bvOff + col] : 0.0f;
-      float *y = (float *)p.Y + yi;
-      *y = ((p.flags & F_STORE) ? 0.0f : *y) + g * (v + b);
-    }
-  }
+  sn_epilogue<MT>(p, sR, nB, tid);
 }
 
-// the longest K a short-call item serves (rounds of 32 units: q4 up to 16 of 1024 k, q8 up to 4 of 2048 k, whose
-// four code loads per unit take 16 registers per round) and its LDS bytes
-constexpr int SN_RND_Q4 = 16, SN_RND_Q8 = 4;
-unsigned gemv_sn_kmax(int we) { return we == W_Q8 ? SN_RND_Q8 * 32u * 64u : SN_RND_Q4 * 32u * 32u; }
+// The short-call items for f16 weights (rows of 16-byte aligned fp16, `ld` and the column offset multiples of 8): units
+// of 64 k, one 128-byte run per row. Lane l of a wave owns rows (l / 8) % 8 and 8 + (l / 8) % 8 of the item and the
+// 16-byte chunk l % 8 (8 k) of each unit; wave w takes the units w, w + 8, w + 16, ..., so one load instruction reads
+// 8 rows x 128 bytes and every load of the item is in flight right after the launch. No X' sums: the dot products of
+// fp16 pairs are the reference's fp32 weight model directly. A row's eight lanes meet by DPP and one lane shuffle.
+template <int XM, int MT, int RND>
+__global__ __launch_bounds__(SN_NT) void k_gemv_sn16(Params p) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rr = (lane >> 3) & 7, cq = lane & 7;
+  const bool glu = p.epi == E_SWIGLU;
+  const uint32_t nit = gridDim.x;
+  const uint32_t item = (nit & 7u) ? blockIdx.x : (blockIdx.x & 7u) * (nit >> 3) + (blockIdx.x >> 3);
+  const uint32_t nB = item * (uint32_t)SN_ROWS;
+  uint32_t woff[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const uint32_t ri = (uint32_t)(rr + 8 * c);
+    const uint32_t wsc = glu ? (ri < 8 ? 2u * ri : 2u * (ri - 8) + 1u) : ri;
+    woff[c] = (wrow(p, nB + wsc) * p.wG + p.wk0) * 2u + 16u * (uint32_t)cq;   // 32-bit: the tensor is below 4 GiB
+  }
+  const srsrc wr = stream_rsrc(p.W);
+  const uint32_t nun = p.K / 64;
+  const uint32_t nb = p.K / 8, nx = MT * nb;
+  u32x4 xv0 = (u32x4){0u, 0u, 0u, 0u};
+  if ((uint32_t)tid < nx && (uint32_t)tid / nb < p.M) xv0 = xload8<XM>(p, tid / nb, RowCtx{0, 0, 0}, 8 * (tid % nb));
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[RND][2];
+#pragma unroll
+  for (int rd = 0; rd < RND; rd++) {
+    uint32_t u = (uint32_t)rd * 8u + (uint32_t)wave;
+    u = u < nun ? u : nun - 1u;
+#pragma unroll
+    for (int c = 0; c < 2; c++) wv[rd][c] = sload128(wr, woff[c] + u * 128u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t sn_smem[];
+  f16 *sX = (f16 *)sn_smem;                                    // [MT][K]
+  for (uint32_t t = tid; t < nx; t += SN_NT) {
+    const uint32_t m = t / nb, kq = t - m * nb;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (t == (uint32_t)tid) v = xv0;
+    else if (m < p.M) v = xload8<XM>(p, m, RowCtx{0, 0, 0}, 8 * kq);
+    *(u32x4 *)(sX + (size_t)m * p.K + 8 * kq) = v;
+  }
+  __syncthreads();
+
+  float acc[2][MT];
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[c][m] = 0.0f;
+#pragma unroll
+  for (int rd = 0; rd < RND; rd++) {
+    const uint32_t u = (uint32_t)rd * 8u + (uint32_t)wave;
+    if (u >= nun) break;                                       // (units ascend with rd)
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      const u32x4 xv = *(const u32x4 *)(sX + (size_t)m * p.K + u * 64u + 8u * (uint32_t)cq);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        float d = acc[c][m];
+        d = __builtin_amdgcn_fdot2(as_h2(wv[rd][c].x), as_h2(xv.x), d, false);
+        d = __builtin_amdgcn_fdot2(as_h2(wv[rd][c].y), as_h2(xv.y), d, false);
+        d = __builtin_amdgcn_fdot2(as_h2(wv[rd][c].z), as_h2(xv.z), d, false);
+        d = __builtin_amdgcn_fdot2(as_h2(wv[rd][c].w), as_h2(xv.w), d, false);
+        acc[c][m] = d;
+      }
+    }
+  }
+  // a row's eight chunk lanes (xor 1, 2 within the quad, then xor 4), then the waves in wave order
+  float *sR = (float *)sn_smem;                                // [wave][MT][16] after a barrier (X' is dead)
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      float v = acc[c][m];
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+      v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+      v += __shfl_xor(v, 4);
+      acc[c][m] = v;
+    }
+  __syncthreads();
+  if (cq == 0) {
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int m = 0; m < MT; m++) sR[(wave * MT + m) * SN_ROWS + rr + 8 * c] = acc[c][m];
+  }
+  __syncthreads();
+  sn_epilogue<MT>(p, sR, nB, tid);
+}
+
+// the longest K a short-call item serves (q4: rounds of 32 units up to 16 of 1024 k; q8: up to 4 rounds of 2048 k, whose
+// four code loads per unit take 16 registers per round; f16: up to 16 rounds of 512 k, 8 registers each) and its LDS
+// bytes
+constexpr int SN_RND_Q4 = 16, SN_RND_Q8 = 4, SN_RND_F16 = 16;
+unsigned gemv_sn_kmax(int we) {
+  return we == W_Q8 ? SN_RND_Q8 * 32u * 64u : we == W_F16 ? SN_RND_F16 * 8u * 64u : SN_RND_Q4 * 32u * 32u;
+}
 // X' and its per-unit sums; after the stream the same buffer holds the waves' partials (8 waves x M x 16 floats)
 uint32_t gemv_sn_lds(int we, uint32_t M, uint32_t K) {
-  const uint32_t x = M * K * 2u + M * (K / (we == W_Q8 ? 64u : 32u)) * 8u, r = (uint32_t)(SN_NT / 64) * M * SN_ROWS * 4u;
+  const uint32_t sums = we == W_F16 ? 0u : M * (K / (we == W_Q8 ? 64u : 32u)) * 8u;
+  const uint32_t x = M * K * 2u + sums, r = (uint32_t)(SN_NT / 64) * M * SN_ROWS * 4u;
   return x > r ? x : r;
 }
 
+template <int XM, int MT>
+static hipError_t launch_sn16_mt(const Params &p, hipStream_t s) {
+  const uint32_t rounds = (p.K / 64u + 7u) / 8u;
+  const uint32_t lds = gemv_sn_lds(W_F16, MT, p.K);
+  const dim3 grid((p.N + SN_ROWS - 1) / SN_ROWS);
+#define SN16_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn16<XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
+  switch (rounds <= 2 ? 2 : rounds <= 4 ? 4 : rounds <= 8 ? 8 : 16) {
+    SN16_CASE(2) SN16_CASE(4) SN16_CASE(8) SN16_CASE(16)
+  default: return hipErrorInvalidValue;
+  }
+#undef SN16_CASE
+  return hipGetLastError();
+}
 template <int WE, int XM, int MT>
 static hipError_t launch_sn_mt(const Params &p, hipStream_t s) {
-  const uint32_t rounds = (p.K / (uint32_t)SnUnit<WE>::UK + 31u) / 32u;
-  const uint32_t lds = gemv_sn_lds(WE, MT, p.K);
-  const dim3 grid((p.N + SN_ROWS - 1) / SN_ROWS);
-#define SN_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn<WE, XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
-  if constexpr (WE == W_Q4) {
-    switch (rounds <= 4 ? 4 : rounds <= 8 ? 8 : rounds <= 12 ? 12 : 16) {
-      SN_CASE(4) SN_CASE(8) SN_CASE(12) SN_CASE(16)
-    default: return hipErrorInvalidValue;
-    }
+  if constexpr (WE == W_F16) {
+    return launch_sn16_mt<XM, MT>(p, s);
   } else {
-    switch (rounds <= 2 ? 2 : 4) {
-      SN_CASE(2) SN_CASE(4)
-    default: return hipErrorInvalidValue;
+    const uint32_t rounds = (p.K / (uint32_t)SnUnit<WE>::UK + 31u) / 32u;
+    const uint32_t lds = gemv_sn_lds(WE, MT, p.K);
+    const dim3 grid((p.N + SN_ROWS - 1) / SN_ROWS);
+#define SN_CASE(R) case R: hipLaunchKernelGGL((k_gemv_sn<WE, XM, MT, R>), grid, dim3(SN_NT), lds, s, p); break;
+    if constexpr (WE == W_Q4) {
+      switch (rounds <= 4 ? 4 : rounds <= 8 ? 8 : rounds <= 12 ? 12 : 16) {
+        SN_CASE(4) SN_CASE(8) SN_CASE(12) SN_CASE(16)
+      default: return hipErrorInvalidValue;
+      }
+    } else {
+      switch (rounds <= 2 ? 2 : 4) {
+        SN_CASE(2) SN_CASE(4)
+      default: return hipErrorInvalidValue;
+      }
     }
-  }
 #undef SN_CASE
-  return hipGetLastError();
+    return hipGetLastError();
+  }
 }
 template <int WE, int XM>
 static hipError_t launch_sn_x(const Params &p, hipStream_t s) {
@@ -744,11 +866,12 @@ static hipError_t launch_sn_w(const Params &p, int xm, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 hipError_t launch_gemv_sn(const Params &p, int we, int xm, hipStream_t s) {
-  const uint32_t uk = we == W_Q8 ? 64u : 32u;
-  if ((we != W_Q4 && we != W_Q8) || p.M == 0 || p.M > 4 || p.K % uk || p.K > gemv_sn_kmax(we) || p.wk0 % uk ||
-      p.epi == E_HEADS || p.epi == E_ONORMGATE || gemv_sn_lds(we, p.M <= 2 ? p.M : 4, p.K) > 64u * 1024u)
+  const uint32_t uk = we == W_Q4 ? 32u : 64u, wk = we == W_F16 ? 8u : uk;
+  if ((we != W_Q4 && we != W_Q8 && we != W_F16) || (we == W_F16 && !(p.flags & F_WALIGN8)) || p.M == 0 || p.M > 4 ||
+      p.K % uk || p.K > gemv_sn_kmax(we) || p.wk0 % wk || p.epi == E_HEADS || p.epi == E_ONORMGATE ||
+      gemv_sn_lds(we, p.M <= 2 ? p.M : 4, p.K) > 64u * 1024u)
     return hipErrorInvalidValue;
-  return we == W_Q4 ? launch_sn_w<W_Q4>(p, xm, s) : launch_sn_w<W_Q8>(p, xm, s);
+  return we == W_Q4 ? launch_sn_w<W_Q4>(p, xm, s) : we == W_Q8 ? launch_sn_w<W_Q8>(p, xm, s) : launch_sn_w<W_F16>(p, xm, s);
 }
 
 // ------------------------------------------------------------------------------------------------------------------

@@ -141,8 +141,10 @@ def test_conv3_frame_window_checked():
 
 def test_kernel_choice():
     assert p0k.select_tile(host_args(make_case(M=1, enc="q4g32a.t64")))["kernel"] == "gemv_short"   # short call
-    assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv_mfma"              # f16 / q8 rows: matrix cores
-    assert p0k.select_tile(host_args(make_case(M=2)))["kernel"] == "gemv_mfma"
+    assert p0k.select_tile(host_args(make_case(M=1)))["kernel"] == "gemv_short"             # f16 rows, 1..4: short call
+    assert p0k.select_tile(host_args(make_case(M=4)))["kernel"] == "gemv_short"
+    assert p0k.select_tile(host_args(make_case(M=5)))["kernel"] == "gemv_mfma"              # 5..16: matrix cores
+    assert p0k.select_tile(host_args(make_case(M=2, K=96)))["kernel"] != "gemv_short"       # K % 64 != 0
     assert p0k.select_tile(host_args(make_case(M=2, enc="q4g32a.t64")))["kernel"] == "gemv_short"
     assert p0k.select_tile(host_args(make_case(M=3, enc="q4g32a.t64")))["kernel"] == "gemv"   # q4, 3..4 rows: stream
     assert p0k.select_tile(host_args(make_case(M=4, enc="q4g32a.t64")))["kernel"] == "gemv"
@@ -234,7 +236,8 @@ def test_short_decode_routing(monkeypatch):
     """q4 decode with one or two rows whose 16-row items number at most about one per CU (1.5 per CU at one row), K up to
     8192 and an element-wise epilogue takes the short-call kernel; q8 decode at one row, and with up to 2 / 1 items per CU at
     2 / 3..4 rows and K up to 8192 as well; P0K_GEMV_SN=0 / 1 switch it off / on wherever it can run (up to 4
-    rows, K up to 16384 for q4 and 8192 for q8, X' in 64 KB of LDS); f16 weights never take it."""
+    rows, K up to 16384 for q4 and 8192 for q8 / f16, X' in 64 KB of LDS); f16 weights with 16-byte rows take it at 1..4
+    rows whenever it can run."""
     q4 = lambda M, N, K, **kw: p0k.select_tile(host_args(make_case(M=M, enc="q4g32a.t64", N=N, K=K, **kw)))["kernel"]   # noqa: E731
     assert q4(1, 4096, 4096) == "gemv_short" and q4(2, 4096, 4096) == "gemv_short"
     assert q4(1, 6144, 4096) == "gemv_short" and q4(2, 6144, 4096) == "gemv"
@@ -246,7 +249,9 @@ def test_short_decode_routing(monkeypatch):
     assert q8(4, 4096, 4096) == "gemv_short" and q8(1, 4096, 8192) == "gemv_short"
     assert q8(2, 10240, 4096) == "gemv_mfma" and q8(4, 6144, 4096) == "gemv_mfma" and q8(1, 4096, 8704) != "gemv_short"
     assert q8(1, 28672, 4096) == "gemv_short" and q8(2, 28672, 4096) == "gemv_mfma"   # 1792 items: 7 per CU
-    assert p0k.select_tile(host_args(make_case(M=1, enc="f16", N=256, K=512)))["kernel"] == "gemv_mfma"
+    f16 = lambda M, N, K, **kw: p0k.select_tile(host_args(make_case(M=M, enc="f16", N=N, K=K, **kw)))["kernel"]   # noqa: E731
+    assert f16(1, 256, 512) == "gemv_short" and f16(4, 14336, 4096) == "gemv_short" and f16(4, 256, 8192) == "gemv_short"
+    assert f16(1, 256, 8256) != "gemv_short" and f16(1, 256, 544) != "gemv_short" and f16(5, 256, 512) != "gemv_short"
     monkeypatch.setenv("P0K_GEMV_SN", "0")
     assert q4(1, 4096, 4096) == "gemv" and q8(1, 4096, 4096) == "gemv_mfma"
     monkeypatch.setenv("P0K_GEMV_SN", "1")

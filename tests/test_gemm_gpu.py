@@ -103,14 +103,14 @@ def test_prologue_epilogue_matrix(dev, M, enc, xmode, epi, kw, monkeypatch):
     banner(f"matrix M={M} {enc} {xmode}/{epi} {kw}")
     c = make_case(enc=enc, xmode=xmode, epi=epi, M=M, N=N, K=K, seed=M + 5, **kw)
     kern = dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"]
-    short = (M <= 2 if enc.startswith("q4") else M <= 4 and enc.startswith("q8")) and epi not in ("heads", "onormgate")
+    short = (M <= 2 if enc.startswith("q4") else M <= 4) and epi not in ("heads", "onormgate")
     assert kern == ("gemv_short" if short else "gemv" if M <= 4 and enc.startswith("q4") else "gemv_mfma" if M <= 16 else
                     "mfma_dma")
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{enc} {xmode}/{epi} M={M}")
     if short:
-        # the one-row / 2-row stream kernel (q4) or the matrix-core decode (q8) on the same call (P0K_GEMV_SN=0)
+        # the one-row / 2-row stream kernel (q4) or the matrix-core decode (q8 / f16) on the same call (P0K_GEMV_SN=0)
         monkeypatch.setenv("P0K_GEMV_SN", "0")
         assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == ("gemv" if enc.startswith("q4") else "gemv_mfma")
         got = c.run_device(dev)
@@ -731,6 +731,36 @@ def test_short_decode_q8_matches_oracle(dev, kw, monkeypatch):
     assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
     got = c.run_device(dev)
     assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short q8 {kw}")
+
+
+SHORT_CASES_F16 = [
+    dict(M=1, N=4096, K=4096, epi="f16"),
+    dict(M=2, N=136, K=128, epi="f32"),
+    dict(M=4, N=40, K=64, epi="f16"),           # one unit: the partials need more LDS than X' does
+    dict(M=3, N=24, K=1088, epi="bias", bias=True, res=True),
+    dict(M=1, N=520, K=8192, epi="resadd", gate=True, bias=True),
+    dict(M=4, N=1024, K=4096, epi="resadd", gate=True, bias=True),
+    dict(M=1, N=512, K=2048, epi="swiglu", bias=True),
+    dict(M=2, N=272, K=3072, epi="swiglu", act="gelu"),
+    dict(M=1, N=256, K=512, epi="resadd", store=True, xmode="rms"),
+    dict(M=2, N=128, K=1024, epi="f16", xmode="lnmod"),
+    dict(M=1, N=200, K=256, epi="f16", ld_pad=8, k0=64, wk0=24, n0=8),
+    dict(M=2, N=96, K=192, epi="swiglu", wr0=64, ld_pad=16),
+]
+
+
+@pytest.mark.parametrize("kw", SHORT_CASES_F16, ids=lambda k: f"M{k['M']}-N{k['N']}-K{k['K']}-{k.get('xmode', 'f16')}-{k['epi']}")
+def test_short_decode_f16_matches_oracle(dev, kw, monkeypatch):
+    """The short-call decode with f16 weights (64-k units of 128-byte row runs, P0K_GEMV_SN=1 forces it): 1..4 rows, K
+    from one unit to its longest (8192), N not a multiple of the item, the element-wise epilogues, rms / lnmod, weight
+    and X offsets; against the oracle."""
+    monkeypatch.setenv("P0K_GEMV_SN", "1")
+    kw = dict(kw)
+    c = make_case(enc="f16", seed=79 + kw["K"] % 83, wscale=0.02, **kw)
+    banner(f"short decode f16 {kw}")
+    assert dev.select_tile(c.args(lambda n: c.bufs[n]))["kernel"] == "gemv_short"
+    got = c.run_device(dev)
+    assert_close(got, c.run_oracle(weights=oracle.CPU_WEIGHTS), fp16=got.dtype == np.uint16, what=f"short f16 {kw}")
 
 
 def test_caller_captured_stream_keeps_its_workspace(dev):
