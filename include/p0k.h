@@ -154,7 +154,7 @@ typedef struct p0k_attn_args {
 } p0k_attn_args;
 
 typedef struct p0k_tile { uint32_t bm, bn; int32_t kernel; } /* kernel: 0 = MFMA GEMM (register-staged), 1 = GEMV (q4, M <= 4), 2 = MFMA GEMV (M <= 16), 3 = MFMA GEMM (load-to-LDS),
-   4 = short-call GEMV (q4 or q8, M <= 4, 16-row items) */
+   4 = short-call GEMV (q4, q8 or f16, M <= 4, 16-row items) */
   p0k_tile;
 
 typedef struct p0k_pool_stats {
