@@ -418,6 +418,26 @@ def test_rowstats(dev):
         dev.free(ds)
 
 
+@pytest.mark.parametrize("rows,cols,ld,c0", [(64, 4096, 4096, 0), (33, 3072, 3080, 8), (5, 8192, 8192, 0),
+                                            (7, 1000, 1004, 4), (3, 9000, 9000, 0), (4, 512, 517, 3)])
+def test_rowstats_shapes(dev, rows, cols, ld, c0):
+    """k_rowstats_reg (aligned rows of up to 8192 columns held in registers: 1..8 pieces per thread, ragged last
+    piece) and k_rowstats (longer or unaligned rows), both modes, against the oracle's two-pass restatement"""
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, ld)) * 1.5 - 0.25).astype(np.float32)
+    for mode in ("ln", "rms"):
+        want = np.zeros(2 * (rows + 2), np.float32)
+        oracle.rowstats(x, rows, cols, mode, 1e-6, want, ld=ld, c0=c0, st_off=2)
+        dx, ds = dev.upload(x), dev.buffer(want.nbytes)
+        try:
+            dev.rowstats(dx, rows, cols, mode, 1e-6, ds, ld=ld, c0=c0, st_off=2)
+            got = dev.read(ds, np.float32, want.size)
+        finally:
+            dev.free(dx)
+            dev.free(ds)
+        assert np.allclose(got, want, rtol=2e-6, atol=2e-6), f"{mode} rows {rows} cols {cols}"
+
+
 def test_pool_reuse_is_zeroed(dev):
     b = dev.upload(np.arange(1000, dtype=np.float32))
     size = b.size
