@@ -68,7 +68,7 @@ MALL = 256 << 20
 FETCH_FACTOR, WRITE_FACTOR = 2.0, 1.0
 TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36003, 28), "decode_q4_swiglu_M1_long": (36003, 28),
                "decode_q4_swiglu_M4": (36123, 112), "decode_q4_swiglu_M16": (37218, 448),
-               "hbm_read_ceiling_73MB": (35851, 0), "hbm_read_ceiling_10MB": (5135, 0), "prefill_rowstats_rms": (16403, 64),
+               "hbm_read_ceiling_73MB": (35851, 0), "hbm_read_ceiling_10MB": (5135, 0), "prefill_rowstats_rms": (16405, 64),
                "decode_q4_plain_M1": (18020, 28), "decode_q4_plain_N4096_M1": (5192, 8), "decode_q8_plain_M1": (29663, 28), "decode_q8_plain_N4096_M1": (8526, 8),
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
