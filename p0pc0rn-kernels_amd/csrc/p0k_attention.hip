@@ -173,7 +173,10 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // m: running maximum in the log2 domain (-1e30: none yet)
     const float mxl = mx <= -1.0e29f ? -1.0e30f : mx * sf;
-    const float mn = fmaxf(m, mxl);
+    // the maximum the exponents subtract stays where it is until some row's maximum grows past it by more than 8
+    // (P <= 2^8 = 256 meanwhile: exact enough in fp16, and O and l keep the same common factor, which the final
+    // division removes), so most tiles skip the rescale of O
+    const float mn = __any(mxl > m + 8.0f) ? fmaxf(m, mxl) : m;
     // a masked score (-1e30) underflows exp2 to 0; a row with no visible key yet subtracts 0 instead of -1e30
     const float mns = mn <= -1.0e29f ? 0.0f : mn;
     float ps = 0.0f;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
         sacc[kb][r] = e;
         ps += e;
       }
-    if (__any(mn != m)) {                                       // rescale only when some row's maximum moved
+    if (__any(mn != m)) {                                       // rescale only when the subtracted maximum moved
       const float alpha = __builtin_amdgcn_exp2f(m - mn);
       l = l * alpha;
 #pragma unroll
