@@ -148,3 +148,54 @@ def test_random_narrow_case_matches_oracle(dev, kw, monkeypatch):
     got = c.run_device(dev)
     want = c.run_oracle()
     assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on 64-column items")
+
+
+def _short_cases(n=48, seed=20251205):
+    """short-call decode items (16 weight rows, every load in flight; P0K_GEMV_SN=1 forces them) over q4 / q8 / f16 with
+    1..4 rows, K up to each encoding's longest (q4 16384, q8 / f16 8192 within 64 KB of X'), ragged N, every
+    element-wise epilogue, the rms / lnmod prologues and the argument offsets"""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        enc = ["q4g32a.t64", "q8g64s.t64", "f16"][rng.integers(3)]
+        M = int(rng.integers(1, 5))
+        kq = 32 if enc == "q4g32a.t64" else 64
+        kmax = 16384 if enc == "q4g32a.t64" else 8192
+        per_k = {32: 2.25, 64: 2.125}[kq] if enc != "f16" else 2.0                        # X' and its unit sums
+        kmax = min(kmax, int(64 * 1024 / ((M if M <= 2 else 4) * per_k)) // kq * kq)        # within 64 KB of LDS
+        K = int(kq * rng.integers(1, kmax // kq + 1))
+        epi = ["f16", "f32", "resadd", "bias", "swiglu"][rng.integers(5)]
+        kw = dict(enc=enc, xmode=["f16", "f16", "rms", "lnmod"][rng.integers(4)], epi=epi, M=M, K=K,
+                  N=(16 if epi == "swiglu" else 8) * int(rng.integers(1, 160)), seed=int(rng.integers(1, 1 << 20)))
+        if epi == "swiglu":
+            kw.update(act=["silu", "gelu"][rng.integers(2)], bias=bool(rng.integers(2)))
+        if epi == "resadd":
+            kw.update(gate=bool(rng.integers(2)), bias=bool(rng.integers(2)), store=bool(rng.integers(2)))
+        if epi == "bias":
+            kw.update(res=bool(rng.integers(2)))
+        if rng.integers(2):
+            kw.update(ld_pad=int(4 * rng.integers(0, 5)), k0=int(4 * rng.integers(0, 9)))
+        if epi != "swiglu" and rng.integers(2):
+            kw.update(n0=int(8 * rng.integers(0, 3)))
+        if rng.integers(3) == 0:
+            kw.update(wk0=(8 if enc == "f16" else kq) * int(rng.integers(1, 3)))
+        if rng.integers(4) == 0:
+            kw.update(wr0=int([1, 16, 64, 100][rng.integers(4)]) if enc == "f16" else 64)
+        out.append(kw)
+    return out
+
+
+SHORT_CASES = _short_cases()
+
+
+@pytest.mark.parametrize("kw", SHORT_CASES, ids=[f"{i:02d}-{k['enc'][:2]}-{k['xmode']}-{k['epi']}-M{k['M']}-N{k['N']}-K{k['K']}"
+                                                 for i, k in enumerate(SHORT_CASES)])
+def test_random_short_case_matches_oracle(dev, kw, monkeypatch):
+    monkeypatch.setenv("P0K_GEMV_SN", "1")
+    c = make_case(**kw)
+    t = dev.select_tile(c.args(lambda n: c.bufs[n]))
+    assert t["kernel"] == "gemv_short", t
+    print(f"[p0k-test] random short case {kw}", flush=True)
+    got = c.run_device(dev)
+    want = c.run_oracle()
+    assert_close(got, want, fp16=got.dtype == np.uint16, what=f"{kw} on 16-row items")
