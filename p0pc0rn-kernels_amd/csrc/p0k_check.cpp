@@ -274,7 +274,9 @@ int prepare_gemm(const p0k_gemm_args *a, Params *out, Plan *plan, std::string *e
   }
   p.flags = f;
 
-  // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M)
+  // ---- kernel choice: the decode GEMV for M <= 16 unless a convolution (whose K order must not depend on M); below,
+  //      the ring kernels first, then the short-call items where sn_rule takes them (q4 short calls, q8 at one row and
+  //      short grids, f16 at 1..4 rows)
   int kernel = K_MFMA;
   unsigned S = 0, KS = 0;
   bool mx = false, narrow = false;
