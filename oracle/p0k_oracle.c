@@ -19,6 +19,7 @@
 #include "p0k_oracle.h"
 
 #include <math.h>
+#include <stddef.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -287,6 +288,27 @@ static uint32_t wrow(const ocfg *c, uint32_t n) {
 
 static uint16_t *y16(const ocfg *c, uint64_t i) { return (uint16_t *)((uint8_t *)c->a->y_buf + c->a->y_off) + i; }
 static float *y32(const ocfg *c, uint64_t i) { return (float *)((uint8_t *)c->a->y_buf + c->a->y_off) + i; }
+
+/* The argument struct this oracle reads, as include/p0k.h lays it out: its size and the byte offset of every field in
+ * declaration order (the tests hold the oracle's own Python flattening of the reference's argument object to it). */
+#define OR_OFF(f) off[n++] = (uint64_t)offsetof(p0k_gemm_args, f)
+uint32_t or_gemm_args_layout(uint64_t *off, uint32_t cap) {
+  uint32_t n = 0;
+  if (cap < 80) return 0;
+  off[n++] = sizeof(p0k_gemm_args);
+  OR_OFF(struct_size); OR_OFF(w_enc); OR_OFF(w_buf); OR_OFF(w_off); OR_OFF(w_bytes); OR_OFF(w_rows); OR_OFF(w_cols);
+  OR_OFF(w_ld); OR_OFF(x_buf); OR_OFF(x_off); OR_OFF(x_size); OR_OFF(x_ld); OR_OFF(x_k0); OR_OFF(x_mode); OR_OFF(y_buf);
+  OR_OFF(y_off); OR_OFF(y_size); OR_OFF(y_ld); OR_OFF(y_n0); OR_OFF(M); OR_OFF(N); OR_OFF(K); OR_OFF(epi); OR_OFF(acc);
+  OR_OFF(tile_bm); OR_OFF(tile_bn); OR_OFF(wr0); OR_OFF(wr1); OR_OFF(wk0); OR_OFF(ev_buf); OR_OFF(ev_off);
+  OR_OFF(ev_size); OR_OFF(st_buf); OR_OFF(st_off); OR_OFF(st_size); OR_OFF(pv_buf); OR_OFF(pv_off); OR_OFF(pv_stride);
+  OR_OFF(pv_size); OR_OFF(bv_buf); OR_OFF(bv_off); OR_OFF(bv_up); OR_OFF(bv_size); OR_OFF(gt_buf); OR_OFF(gt_size);
+  OR_OFF(rope_buf); OR_OFF(rope_size); OR_OFF(res); OR_OFF(store); OR_OFF(act); OR_OFF(h_Ltot); OR_OFF(h_Hq);
+  OR_OFF(h_Hkv); OR_OFF(h_rowOff); OR_OFF(h_eps); OR_OFF(h_rope_mode); OR_OFF(c_Hi); OR_OFF(c_Wi); OR_OFF(c_Ci);
+  OR_OFF(c_Ho); OR_OFF(c_Wo); OR_OFF(c_stride); OR_OFF(c_padT); OR_OFF(c_padL); OR_OFF(c_ks); OR_OFF(c_up2);
+  OR_OFF(c_gn); OR_OFF(c_pn);
+  return n;
+}
+#undef OR_OFF
 
 int or_gemm(const p0k_gemm_args *a, uint32_t m0, uint32_t m1) {
   if (!a || !a->x_buf || !a->w_buf || !a->y_buf || a->K % 32) return -1;

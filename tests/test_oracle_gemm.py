@@ -273,3 +273,33 @@ def test_oracle_rowstats():
     s = st.reshape(-1, 2)[:7]
     assert np.all(s[:, 0] == 0)
     assert np.allclose(s[:, 1], 1 / np.sqrt((xx ** 2).mean(1) + 1e-6), rtol=1e-6)
+
+
+def test_oracle_args_layout_is_the_header_s():
+    """The oracle flattens the reference's argument object by its own code (oracle.oracle_args): its struct has the
+    size and the field offsets of p0k_gemm_args as the C oracle was compiled against include/p0k.h"""
+    import ctypes as C
+    size, offs = oracle.args_layout()
+    fields = oracle.OracleArgs._fields_
+    assert size == C.sizeof(oracle.OracleArgs) and len(offs) == len(fields)
+    for (name, _), off in zip(fields, offs):
+        assert getattr(oracle.OracleArgs, name).offset == off, name
+
+
+def test_oracle_and_product_flatten_alike():
+    """The checker's flattening (oracle.oracle_args) and the product's (p0k.gemm_args) are two separate restatements of
+    the reference's argument object; over the randomised parity cases, the GLU and short-call sweeps, conv / conv3 and
+    heads calls, every byte of the two structs agrees"""
+    import p0k
+    import test_random_cases as R
+    kws = R.CASES + R.GLU_CASES + R.SHORT_CASES + R.NARROW_CASES
+    cases = [make_case(**kw) for kw in kws[:120]]
+    cases += [make_conv3_case(T=3, H=5, W=7, C=64, N=128, pn=pn) for pn in (False, True)]
+    cases += [make_conv2d_case(**kw) for kw in ({}, {"up2": True}, {"gn": True})]
+    cases += [make_case(enc="q4g32a.t64", xmode="lnmod", epi="heads", M=40, N=4 * 128, K=256, Hq=2, Hkv=1,
+                        rope_mode=m, row_off=3) for m in ("interleaved", "half")]
+    for c in cases:
+        a = c.args(lambda n: c.bufs[n])
+        want = bytes(p0k.gemm_args(a, p0k.numpy_resolve))
+        got = bytes(oracle.oracle_args(a))
+        assert got == want, c.spec
