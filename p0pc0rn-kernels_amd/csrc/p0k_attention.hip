@@ -217,14 +217,8 @@ __global__ __launch_bounds__((2 * AT_BQ), (512 / (2 * AT_BQ))) void k_attention(
         oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bp, oacc[db], 0, 0, 0);
       }
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-#pragma unroll
-    for (int q = 0; q < 15; q++) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_barrier(0);
+    // (this phase is left to the compiler's schedule: pinning each MFMA behind two transposed V reads, as the S phase
+    // pins its K reads, ran 249-251 against 242-244 us)
     if (t + AT_S - 1 < ntile) __builtin_amdgcn_s_waitcnt(WAIT_RING);   // this wave's share of tile t + 1 has landed
     else __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
