@@ -73,7 +73,7 @@ TRAFFIC_KIB = {"decode_q4_swiglu_M1": (36003, 28), "decode_q4_swiglu_M1_long": (
                # MFMA workloads: every kernel of one call (prologue pass + GEMM launches)
                "prefill_q8_rms_resadd": (82670, 49152), "prefill_q8_rms_bias_f16res": (74494, 32768),
                "dit_qkv_q4_lnmod_heads": (132062, 98304), "dit_up_q4_geglu": (250812, 98304),
-               "conv3_128_T13x92x160": (168504, 47840), "dit_attention_24x4096": (36917, 25593)}
+               "conv3_128_T13x92x160": (168504, 47840), "dit_attention_24x4096": (36917, 26433)}
 
 
 def log(msg):
