@@ -116,3 +116,36 @@ def test_attention_matches_oracle(dev, c, bq, monkeypatch):
     finally:
         for d in (dq, dk, dv, do):
             dev.free(d)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("pattern", ["slow ramp", "fast ramp", "late spike", "falling"])
+def test_attention_moving_maximum(dev, pattern):
+    """Scores whose row maximum keeps moving across the 64-key tiles: the kernel keeps the subtracted maximum until a
+    row's maximum outgrows it by more than 8 in the log2 domain (P up to 2^8 meanwhile) and rescales O and l when it
+    moves. Every query sees s_j = g(j) + noise: a slow ramp (about 4 log2 units per tile: the maximum moves every other
+    tile), a fast ramp (16 per tile: every tile), one late spike (25 units in one tile) and a falling ramp (the maximum
+    is set by the first tile and never moves); against float64 numpy with the file's fp16 tolerance."""
+    Hq, Lq, Lk, D = 2, 128, 512, 128
+    j = np.arange(Lk, dtype=np.float64)
+    g = {"slow ramp": 0.5 * j, "fast ramp": 2.0 * j, "late spike": np.where(j == 300, 200.0, 0.0),
+         "falling": 60.0 - 0.1 * j}[pattern]
+    rng = np.random.default_rng(7)
+    # q = (1, ..., 1) + noise, k_j = g(j) / 128 (1, ..., 1) + noise: q . k_j = g(j) + O(noise)
+    Q = np.ones((Hq, Lq, D)) + 0.05 * rng.standard_normal((Hq, Lq, D))
+    K = np.repeat((g / 128.0)[None, :, None], D, axis=2).repeat(Hq, axis=0) + 0.05 * rng.standard_normal((Hq, Lk, D))
+    V = rng.standard_normal((Hq, Lk, D))
+    q, k, v = (oracle.f16_bits(a.astype(np.float32).ravel()) for a in (Q, K, V))
+    c = dict(Hq=Hq, Hkv=Hq, Lq=Lq, Lk=Lk, mode=0)
+    dq, dk, dv, do = dev.upload(q), dev.upload(k), dev.upload(v), dev.buffer(Lq * Hq * D * 2)
+    try:
+        dev.attention({"q": {"buf": dq}, "k": {"buf": dk}, "v": {"buf": dv}, "o": {"buf": do}, "Lq": Lq, "Lk": Lk,
+                       "Hq": Hq, "Hkv": Hq})
+        got = oracle.h2f(dev.read(do, np.uint16, Lq * Hq * D))
+    finally:
+        for d in (dq, dk, dv, do):
+            dev.free(d)
+    want = numpy_attention(q, k, v, c).ravel()
+    err = np.abs(got - want)
+    bound = 2 ** -8 * np.abs(want).max() + 2 ** -9 * np.abs(want)
+    assert np.all(err <= bound), f"{pattern}: max err {err.max()} (bound {bound.max()})"
